@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput of the MI355X MoE feed-forward path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-extra] [--no-cpu]
+
+A step is one pass of the MoE block over one batch of synthetic input with all
+weights and inputs resident in HBM:
+  olmoe_decode_t8_x16 (default, the headline line): 8 tokens through 16
+  independent OLMoE MoE layers (hidden 2048, 64 experts, top-8, intermediate
+  1024, 4-bit affine g=64 experts, bf16 scales/biases).
+`value` is MoE-layer tok/s = tokens x layers / step time.
+
+The other workloads (decode 1 token, prefill 512, prefill 4096 with Zipf
+routing, Granite prefill 2048 and decode 32) are measured in the same run and
+reported under "per_workload". Each reports per-layer latency, tok/s, the
+algorithmic bytes (routed experts counted from the step's own routing) and
+FLOPs, and its roofline fraction (HBM for decode, bf16 MFMA for prefill).
+
+"roofline" is for the dominant kernel of the headline workload, timed with HIP
+events around each of its launches on the stream it runs on. "cpu_baseline"
+is the oracle's MLX-semantics CPU block on the host cores over a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "MoE-layer tok/s: decode b=1 & prefill 4096; % HBM BW / % MFMA peak"
+HEADLINE = "olmoe_decode_t8_x16"
+DECODE = {"olmoe_decode_t1", "olmoe_decode_t8_x16", "granite_decode_t32"}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default=HEADLINE)
+    p.add_argument("--no-extra", action="store_true", help="measure the headline workload only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--deterministic", action="store_true", help="ordered K reduction in prefill")
+    return p.parse_args()
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return model, cores
+
+
+class Runner:
+    """Resident weights/input of one workload and its step function."""
+
+    def __init__(self, name, device, deterministic=False):
+        import torch
+
+        from trifuse_amd import moe as tmoe
+        from trifuse_amd import workload as wl
+
+        self.torch = torch
+        self.wl = wl.WORKLOADS[name]
+        g = self.wl.geometry
+        self.geom = g
+        self.layers = wl.workload_layers(self.wl, device)
+        self.weights = [tmoe.ExpertWeights.from_layer(l) for l in self.layers]
+        self.x = wl.workload_x(self.wl).to(device)
+        self.block = tmoe.MoEBlock(g.hidden, g.intermediate, g.experts, g.top_k, route=g.route)
+        self.block.workspace(self.wl.tokens, device)
+        self.y = None
+        self.deterministic = deterministic
+
+    def step(self):
+        for w in self.weights:
+            self.y = self.block.forward(self.x, w, deterministic=self.deterministic)
+
+    def distinct_experts(self):
+        """Distinct experts routed per layer, from the GPU's own routing."""
+        out = []
+        for w in self.weights:
+            _, idx, _ = self.block.forward(self.x, w, return_routes=True)
+            out.append(int(self.torch.unique(idx).numel()))
+        return out
+
+    def time_steps(self, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            self.step()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return start.elapsed_time(end) / steps, wall * 1e3 / steps
+
+    def stage_times(self, steps):
+        from trifuse_amd.moe import StageProfiler
+
+        prof = StageProfiler(capacity=steps * len(self.weights) * 6 + 16)
+        with prof:
+            for _ in range(steps):
+                self.step()
+        self.torch.cuda.synchronize()
+        out = {}
+        for s in prof.STAGES:
+            ms, n = prof.stage(s)
+            if n:
+                out[s] = {"us_per_launch": ms * 1e3 / n, "launches": n}
+        prof.close()
+        return out
+
+
+def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages):
+    from trifuse_amd import workload as wl
+
+    g, T, L = r.geom, r.wl.tokens, r.wl.layers
+    U = r.distinct_experts()
+    per_layer_ms = ms_per_step / L
+    bytes_step = sum(wl.algorithmic_bytes(g, T, u) for u in U)
+    flops_step = wl.algorithmic_flops(g, T) * L
+    gbs = bytes_step / (ms_per_step * 1e-3) / 1e9
+    tflops = flops_step / (ms_per_step * 1e-3) / 1e12
+    bound = "hbm" if r.wl.name in DECODE else "mfma"
+    rep = {
+        "description": r.wl.description,
+        "tokens": T, "layers": L,
+        "per_layer_us": per_layer_ms * 1e3,
+        "tok_per_s": T * L / (ms_per_step * 1e-3),
+        "wall_ms_per_step": wall_ms,
+        "distinct_experts_per_layer": U if L <= 4 else [min(U), sum(U) / len(U), max(U)],
+        "alg_bytes_per_step": bytes_step,
+        "alg_flops_per_step": flops_step,
+        "hbm_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+        "mfma_TFLOPs": tflops, "mfma_frac": tflops / BF16_PEAK_TFLOPS,
+        "bound": bound,
+        "stages_us": {k: round(v["us_per_launch"], 3) for k, v in stages.items()},
+    }
+    return rep
+
+
+def dominant_roofline(r: Runner, stages):
+    """Roofline object for the gate/up kernel (the largest share of bytes and FLOPs)."""
+    from trifuse_amd import workload as wl
+
+    g, T = r.geom, r.wl.tokens
+    st = stages["gateup"]
+    dur_s = st["us_per_launch"] * 1e-6
+    U = r.distinct_experts()
+    H, I = g.hidden, g.intermediate
+    gu_bytes_expert = 2 * (I * H // 2 + 2 * (I * H // 64) * 2)
+    if r.wl.name in DECODE:
+        # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
+        per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
+        achieved = per_launch / dur_s / 1e9
+        return {"kernel": "gemv_kernel<gateup>", "bound": "hbm", "achieved": achieved,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                "traffic": None, "alg_bytes_per_launch": per_launch,
+                "us_per_launch": st["us_per_launch"]}
+    flops = wl.gemm_flops(g, T * g.top_k, "gateup")
+    achieved = flops / dur_s / 1e12
+    return {"kernel": "ggemm_kernel<gateup>", "bound": "mfma", "achieved": achieved,
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
+            "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}
+
+
+def cpu_baseline(r: Runner, seconds: float):
+    """The oracle's MLX-semantics CPU block on the host cores over a bounded
+    sample: whole layers of the same workload (first layers first) until
+    `seconds` have elapsed, at least one."""
+    import numpy as np
+
+    import oracle
+
+    model, cores = cpu_info()
+    threads = min(cores, 64)
+    T = r.wl.tokens
+    done_tokens = 0
+    layers = 0
+    elapsed = 0.0
+    used = threads
+    x = r.x.cpu().view(r.torch.int16).numpy().view(np.uint16)
+
+    class NpLayer:
+        pass
+
+    for lay in r.layers:
+        nl = NpLayer()
+        for name in ("gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q", "down_s", "down_b"):
+            t = getattr(lay, name).cpu()
+            setattr(nl, name, t.numpy() if t.dtype == r.torch.int32 else t.view(r.torch.int16).numpy())
+        router = lay.router.cpu().view(r.torch.int16).numpy()
+        lb = None if lay.logit_bias is None else lay.logit_bias.cpu().numpy()
+        t0 = time.perf_counter()
+        _, _, _, used = oracle.moe_block_cpu(x, nl, r.geom.route, router, lb, top_k=r.geom.top_k,
+                                             threads=threads)
+        elapsed += time.perf_counter() - t0
+        done_tokens += T
+        layers += 1
+        if elapsed >= seconds:
+            break
+    return {"value": done_tokens / elapsed, "unit": "tok/s", "cores": used, "kind": "port",
+            "sample": f"{layers} of {r.wl.layers} layers x {T} tokens of {r.wl.name}, "
+                      f"{elapsed:.1f} s, {used} OpenMP threads on {model}",
+            "per_layer_ms": elapsed / layers * 1e3}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The design note on sharding describes how the MoE path would split over GPUs.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    log(f"[bench] workload {args.workload}: building resident weights")
+    head = Runner(args.workload, dev, args.deterministic)
+    ms, wall = head.time_steps(args.steps, args.warmup)
+    log(f"[bench] {args.workload}: {ms * 1e3:.1f} us/step")
+    stages = head.stage_times(max(10, min(args.steps, 100)))
+    report = workload_report(head, ms, wall, stages)
+    roof = dominant_roofline(head, stages)
+
+    per = {args.workload: report}
+    if not args.no_extra:
+        from trifuse_amd import workload as wl
+
+        for name, w in wl.WORKLOADS.items():
+            if name == args.workload:
+                continue
+            log(f"[bench] workload {name}")
+            r = Runner(name, dev, args.deterministic)
+            steps = args.steps if name in DECODE else max(20, args.steps // 4)
+            m, wa = r.time_steps(steps, max(3, args.warmup // 2))
+            st = r.stage_times(10)
+            per[name] = workload_report(r, m, wa, st)
+            per[name]["roofline_gateup"] = dominant_roofline(r, st)
+            if not args.no_cpu and name in ("olmoe_prefill_t4096_zipf", "olmoe_decode_t1"):
+                per[name]["cpu_baseline"] = cpu_baseline(r, 3.0)
+            del r
+            torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(head, args.cpu_seconds)
+
+    g = head.geom
+    line = {
+        "metric": METRIC,
+        "value": report["tok_per_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "hidden": g.hidden, "experts": g.experts,
+                   "top_k": g.top_k, "intermediate": g.intermediate, "tokens": head.wl.tokens,
+                   "layers": head.wl.layers, "weights": "4-bit affine g64, bf16 scales/biases",
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_workload": per,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,648 @@
+// C ABI: plans, workspace layout, argument checks and launch orchestration.
+//
+// Orchestration follows NativeGraniteMoEPrefill::moe
+// (MLXNativeGraniteMoEPrefill.h:627-702): router linear, route, grouping,
+// up/gate expert matmuls with SwiGLU, down expert matmul, weighted combine and
+// residual. The grouping is always the stable expert sort (the reference sorts
+// once T*K >= 64; with fewer routes it gathers per route, which yields the
+// same per-route results).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "tfm_internal.h"
+
+struct tfm_plan {
+  tfm_geometry g;
+  int device;
+  int gemv_max_routes;  // route count up to which the decode GEMV path is used
+};
+
+// Stage profiler: HIP events recorded around each kernel stage of the calls
+// made on a thread while the profiler is attached to it.
+struct tfm_profiler {
+  int capacity = 0;
+  int used = 0;
+  int dropped = 0;
+  std::vector<hipEvent_t> start, end;
+  std::vector<int> stage;
+};
+
+namespace tfm {
+
+static thread_local std::string g_last_error;
+static thread_local tfm_profiler* g_profiler = nullptr;
+
+// Records the stage's start event on construction and its end event on
+// destruction when a profiler is attached to the calling thread.
+struct StageScope {
+  tfm_profiler* p;
+  int slot = -1;
+  hipStream_t s;
+  StageScope(int stage_id, hipStream_t stream) : p(g_profiler), s(stream) {
+    if (!p) return;
+    if (p->used >= p->capacity) {
+      ++p->dropped;
+      return;
+    }
+    slot = p->used++;
+    p->stage[slot] = stage_id;
+    (void)hipEventRecord(p->start[slot], s);
+  }
+  ~StageScope() {
+    if (slot >= 0) (void)hipEventRecord(p->end[slot], s);
+  }
+  StageScope(const StageScope&) = delete;
+  StageScope& operator=(const StageScope&) = delete;
+};
+
+void set_last_error(const std::string& message) { g_last_error = message; }
+
+[[noreturn]] void fail(int code, const std::string& message) { throw Error{code, message}; }
+
+void check_hip(hipError_t err, const char* what) {
+  if (err != hipSuccess) fail(TFM_E_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+template <typename F>
+static int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return TFM_OK;
+  } catch (const Error& e) {
+    g_last_error = e.message;
+    return e.code;
+  } catch (const std::exception& e) {
+    g_last_error = std::string("internal error: ") + e.what();
+    return TFM_E_INVALID;
+  } catch (...) {
+    g_last_error = "internal error";
+    return TFM_E_INVALID;
+  }
+}
+
+static void need(bool ok, const std::string& message) {
+  if (!ok) fail(TFM_E_INVALID, message);
+}
+
+static void check_geometry(const tfm_geometry& g) {
+  need(g.hidden_size > 0 && g.hidden_size % 64 == 0, "hidden_size must be a positive multiple of 64");
+  need(g.intermediate_size > 0 && g.intermediate_size % 64 == 0,
+       "intermediate_size must be a positive multiple of 64");
+  need(g.num_experts > 0, "num_experts must be positive");
+  need(g.experts_per_token > 0 && g.experts_per_token <= g.num_experts,
+       "experts_per_token must be in [1, num_experts]");
+  need(g.route == TFM_ROUTE_OLMOE || g.route == TFM_ROUTE_GRANITE, "unknown route kind");
+  need(g.router == TFM_ROUTER_DENSE || g.router == TFM_ROUTER_AFFINE, "unknown router kind");
+  need(g.dtype == TFM_DTYPE_BF16 || g.dtype == TFM_DTYPE_F16, "unknown dtype");
+  need(g.bits == 4 || g.bits == 8, "bits must be 4 or 8");
+  need(g.group_size == 32 || g.group_size == 64 || g.group_size == 128,
+       "group_size must be 32, 64 or 128");
+  if (g.num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built (wave-wide routing)");
+  if (g.dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 activations/scales are built");
+  if (g.router != TFM_ROUTER_DENSE) fail(TFM_E_UNSUPPORTED, "only the dense router is built");
+  if (g.bits != 4) fail(TFM_E_UNSUPPORTED, "only 4-bit weights are built");
+  if (g.group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
+}
+
+// Workspace of the MoE block for T tokens. base == nullptr computes sizes.
+struct BlockWs {
+  WsHeader* hdr;
+  uint16_t* logits;
+  int32_t* idx;
+  float* gates;
+  Grouping grp;
+  uint16_t* h;
+  float* P;  // [R, H] sorted rows; the atomic path uses its start as acc [T, H]
+  size_t bytes;
+};
+
+static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
+  const int64_t R = T * g.experts_per_token;
+  Carver c(base);
+  BlockWs w{};
+  w.hdr = c.take<WsHeader>(1);
+  w.logits = c.take<uint16_t>((size_t)(T * g.num_experts));
+  w.idx = c.take<int32_t>((size_t)R);
+  w.gates = c.take<float>((size_t)R);
+  w.grp.order = c.take<int32_t>((size_t)R);
+  w.grp.inverse = c.take<int32_t>((size_t)R);
+  w.grp.offsets = c.take<int32_t>((size_t)g.num_experts + 1);
+  w.grp.active = c.take<int32_t>((size_t)g.num_experts + 1);
+  w.grp.E = g.num_experts;
+  w.h = c.take<uint16_t>((size_t)(R * g.intermediate_size));
+  w.P = c.take<float>((size_t)(R * g.hidden_size));
+  w.bytes = align_up(c.offset, 256);
+  return w;
+}
+
+struct GroupWs {
+  WsHeader* hdr;
+  Grouping grp;
+  size_t bytes;
+};
+
+static GroupWs carve_group(int64_t n, int E, void* base) {
+  Carver c(base);
+  GroupWs w{};
+  w.hdr = c.take<WsHeader>(1);
+  w.grp.order = c.take<int32_t>((size_t)n);
+  w.grp.inverse = c.take<int32_t>((size_t)n);
+  w.grp.offsets = c.take<int32_t>((size_t)E + 1);
+  w.grp.active = c.take<int32_t>((size_t)E + 1);
+  w.grp.E = E;
+  w.bytes = align_up(c.offset, 256);
+  return w;
+}
+
+static void need_ws(void* ws, size_t have, size_t want) {
+  if (!ws) fail(TFM_E_WORKSPACE, "workspace is null");
+  if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) fail(TFM_E_WORKSPACE, "workspace must be 256-byte aligned");
+  if (have < want)
+    fail(TFM_E_WORKSPACE, "workspace too small: " + std::to_string(have) + " < " + std::to_string(want));
+}
+
+static void need_ptr(const void* p, const char* name) {
+  if (!p) fail(TFM_E_INVALID, std::string(name) + " is null");
+}
+
+static void need_align16(const void* p, const char* name) {
+  if (reinterpret_cast<uintptr_t>(p) & 15) fail(TFM_E_INVALID, std::string(name) + " must be 16-byte aligned");
+}
+
+static void check_affine(const tfm_affine& a, const char* name) {
+  need_ptr(a.q, name);
+  need_ptr(a.scales, name);
+  need_ptr(a.biases, name);
+  need_align16(a.q, name);
+}
+
+static int gemv_threshold() {
+  static int v = [] {
+    const char* s = std::getenv("TFM_GEMV_MAX_ROUTES");
+    if (!s) return 256;
+    char* end = nullptr;
+    const long n = std::strtol(s, &end, 10);
+    if (!end || *end != 0 || n < 0 || n > (1 << 30)) {
+      std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_GEMV_MAX_ROUTES=%s\n", s);
+      return 256;
+    }
+    return (int)n;
+  }();
+  return v;
+}
+
+// Expert part of the block on grouped routes (flat routes t*K+k of idx).
+static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const uint16_t* residual,
+                        const int32_t* idx, const float* gates, const tfm_moe_weights* w,
+                        uint16_t* y, uint32_t flags, BlockWs& ws, hipStream_t s) {
+  const tfm_geometry& g = p->g;
+  const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
+  const int64_t R = T * K;
+  {
+    StageScope st(TFM_STAGE_GROUP, s);
+    launch_group(idx, R, E, ws.grp, &ws.hdr->status, s);
+  }
+  const int max_active = (int)(R < E ? R : E);
+  const RowMap rm{ws.grp.order, nullptr, K, T, &ws.hdr->status};
+  if (R <= p->gemv_max_routes) {
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_gemv_gateup(x, rm, ws.grp, max_active, R, w->gate, w->up, I, H, ws.h, s);
+    }
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_gemv_scaled(ws.h, ws.grp, max_active, R, w->down, H, I, gates, ws.P, s);
+    }
+    StageScope st(TFM_STAGE_COMBINE, s);
+    launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
+                          g.residual_multiplier, y, s);
+  } else if (flags & TFM_FLAG_DETERMINISTIC) {
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, nullptr, 0, s);
+    }
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, gates, K, nullptr, ws.P, s);
+    }
+    StageScope st(TFM_STAGE_COMBINE, s);
+    launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
+                          g.residual_multiplier, y, s);
+  } else {
+    float* acc = ws.P;
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, acc, T * H, s);
+    }
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, gates, K, acc, nullptr, s);
+    }
+    StageScope st(TFM_STAGE_COMBINE, s);
+    launch_finalize_acc(acc, (int)T, H, residual, g.residual_multiplier, y, s);
+  }
+}
+
+static void check_weights(const tfm_moe_weights* w, bool router) {
+  need_ptr(w, "weights");
+  if (router) {
+    need_ptr(w->router, "weights->router");
+    need_align16(w->router, "weights->router");
+  }
+  check_affine(w->gate, "weights->gate");
+  check_affine(w->up, "weights->up");
+  check_affine(w->down, "weights->down");
+}
+
+}  // namespace tfm
+
+using namespace tfm;
+
+extern "C" {
+
+const char* tfm_last_error(void) { return g_last_error.c_str(); }
+
+const char* tfm_version(void) { return "trifuse_moe 0.1 gfx950"; }
+
+int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
+  return guarded([&] {
+    need_ptr(geometry, "geometry");
+    need_ptr(plan_out, "plan_out");
+    *plan_out = nullptr;
+    check_geometry(*geometry);
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    tfm_plan* p = new tfm_plan{};
+    p->g = *geometry;
+    p->device = dev;
+    p->gemv_max_routes = gemv_threshold();
+    *plan_out = p;
+  });
+}
+
+void tfm_plan_destroy(tfm_plan* plan) { delete plan; }
+
+size_t tfm_workspace_bytes(const tfm_plan* plan, int64_t tokens) {
+  if (!plan || tokens < 0) return 0;
+  return carve_block(plan->g, tokens, nullptr).bytes;
+}
+
+size_t tfm_group_workspace_bytes(int64_t n_routes, int32_t num_experts) {
+  if (n_routes < 0 || num_experts <= 0) return 0;
+  return carve_group(n_routes, num_experts, nullptr).bytes;
+}
+
+int tfm_route(const tfm_plan* plan, const void* x, int64_t tokens, const void* router,
+              const float* logit_bias, void* logits, int32_t* idx, void* gates, void* workspace,
+              size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    if (tokens == 0) return;
+    need_ptr(x, "x");
+    need_ptr(router, "router");
+    need_ptr(idx, "idx");
+    need_align16(x, "x");
+    need_align16(router, "router");
+    const tfm_geometry& g = plan->g;
+    BlockWs ws = carve_block(g, tokens, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : ws.logits;
+    launch_router_logits(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router),
+                         logit_bias, (int)tokens, g.hidden_size, g.num_experts, lg, s);
+    launch_topk(g.route, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates, nullptr, s);
+  });
+}
+
+int tfm_route_logits(const tfm_plan* plan, const void* logits, int64_t tokens, int32_t* idx,
+                     void* gates, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    if (tokens == 0) return;
+    need_ptr(logits, "logits");
+    need_ptr(idx, "idx");
+    const tfm_geometry& g = plan->g;
+    launch_topk(g.route, static_cast<const uint16_t*>(logits), (int)tokens, g.num_experts,
+                g.experts_per_token, idx, gates, nullptr, static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_topk(const void* values, int64_t tokens, int32_t n, int32_t k, int32_t rule,
+             int32_t dtype, int32_t* idx, void* stream) {
+  return guarded([&] {
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    need(n > 0 && k > 0 && k <= n, "need 0 < k <= n");
+    need(rule == TFM_ROUTE_OLMOE || rule == TFM_ROUTE_GRANITE, "unknown top-k rule");
+    if (n > 64) fail(TFM_E_UNSUPPORTED, "top-k over more than 64 values is not built");
+    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    if (tokens == 0) return;
+    need_ptr(values, "values");
+    need_ptr(idx, "idx");
+    launch_rank_topk(rule, static_cast<const uint16_t*>(values), (int)tokens, n, k, idx,
+                     static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_olmoe_softmax(const void* logits, int64_t tokens, int32_t num_experts, int32_t dtype,
+                      void* probs, void* stream) {
+  return guarded([&] {
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    need(num_experts > 0, "num_experts must be positive");
+    if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
+    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    if (tokens == 0) return;
+    need_ptr(logits, "logits");
+    need_ptr(probs, "probs");
+    launch_olmoe_softmax(static_cast<const uint16_t*>(logits), (int)tokens, num_experts,
+                         static_cast<uint16_t*>(probs), static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_group(const int32_t* expert_ids, int64_t n_routes, int32_t num_experts, int32_t* order,
+              int32_t* inverse, int32_t* offsets, void* workspace, size_t workspace_bytes,
+              void* stream) {
+  return guarded([&] {
+    need(n_routes >= 0 && n_routes <= INT32_MAX, "n_routes out of range");
+    need(num_experts > 0, "num_experts must be positive");
+    if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
+    need_ptr(offsets, "offsets");
+    GroupWs ws = carve_group(n_routes, num_experts, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    if (n_routes > 0) {
+      need_ptr(expert_ids, "expert_ids");
+      need_ptr(order, "order");
+      need_ptr(inverse, "inverse");
+    }
+    Grouping gout = ws.grp;
+    gout.order = order;
+    gout.inverse = inverse;
+    gout.offsets = offsets;
+    launch_group(expert_ids, n_routes, num_experts, gout, &ws.hdr->status,
+                 static_cast<hipStream_t>(stream));
+  });
+}
+
+size_t tfm_gather_qmm_workspace_bytes(int64_t rows, int32_t num_experts, int32_t n_out,
+                                      int32_t k_in) {
+  (void)n_out;
+  (void)k_in;
+  if (rows < 0 || num_experts <= 0) return 0;
+  return carve_group(rows, num_experts, nullptr).bytes;
+}
+
+int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
+                   const int32_t* rhs_indices, int64_t rows,
+                   const tfm_affine* w, int32_t num_experts, int32_t n_out, int32_t k_in,
+                   int32_t group_size, int32_t bits, int32_t dtype, int32_t sorted, void* out,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  (void)sorted;
+  return guarded([&] {
+    need(rows >= 0 && rows <= INT32_MAX, "rows out of range");
+    need(x_row_count >= 0, "x_row_count out of range");
+    need(x_rows || x_row_count >= rows, "x_row_count < rows with identity x_rows");
+    need(num_experts > 0, "num_experts must be positive");
+    need(n_out > 0 && k_in > 0, "n_out and k_in must be positive");
+    need(bits == 4 || bits == 8, "bits must be 4 or 8");
+    need(group_size == 32 || group_size == 64 || group_size == 128, "group_size must be 32, 64 or 128");
+    need(k_in % group_size == 0, "k_in must be a multiple of group_size");
+    if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
+    if (bits != 4 || group_size != 64) fail(TFM_E_UNSUPPORTED, "only 4-bit group-64 weights are built");
+    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    if (n_out % 64 != 0) fail(TFM_E_UNSUPPORTED, "n_out must be a multiple of 64");
+    GroupWs ws = carve_group(rows, num_experts, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    if (rows == 0) return;
+    need_ptr(x, "x");
+    need_ptr(rhs_indices, "rhs_indices");
+    need_ptr(w, "w");
+    need_ptr(out, "out");
+    need_align16(x, "x");
+    check_affine(*w, "w");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    launch_group(rhs_indices, rows, num_experts, ws.grp, &ws.hdr->status, s);
+    // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
+    const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
+    const int max_active = (int)(rows < num_experts ? rows : num_experts);
+    if (rows <= gemv_threshold())
+      launch_gemv_plain(static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
+                        static_cast<uint16_t*>(out), s);
+    else
+      launch_ggemm_plain(static_cast<const uint16_t*>(x), rm, ws.grp, rows, num_experts, *w, n_out,
+                         k_in, static_cast<uint16_t*>(out), s);
+  });
+}
+
+int tfm_moe_experts(const tfm_plan* plan, const void* x, int64_t tokens, const void* residual,
+                    const int32_t* idx, const float* gates, const tfm_moe_weights* weights, void* y,
+                    uint32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    if (tokens == 0) return;
+    need_ptr(x, "x");
+    need_ptr(idx, "idx");
+    need_ptr(gates, "gates");
+    need_ptr(y, "y");
+    need_align16(x, "x");
+    need_align16(y, "y");
+    if (residual) need_align16(residual, "residual");
+    check_weights(weights, false);
+    BlockWs ws = carve_block(plan->g, tokens, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
+                idx, gates, weights, static_cast<uint16_t*>(y), flags, ws,
+                static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const void* residual,
+                    const tfm_moe_weights* weights, void* y, int32_t* idx_out, float* gates_out,
+                    uint32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    if (tokens == 0) return;
+    need_ptr(x, "x");
+    need_ptr(y, "y");
+    need_align16(x, "x");
+    need_align16(y, "y");
+    if (residual) need_align16(residual, "residual");
+    check_weights(weights, true);
+    const tfm_geometry& g = plan->g;
+    BlockWs ws = carve_block(g, tokens, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t R = tokens * g.experts_per_token;
+    {
+      StageScope st(TFM_STAGE_ROUTER, s);
+      launch_router_logits(static_cast<const uint16_t*>(x),
+                           static_cast<const uint16_t*>(weights->router), weights->logit_bias,
+                           (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+    }
+    {
+      StageScope st(TFM_STAGE_TOPK, s);
+      launch_topk(g.route, ws.logits, (int)tokens, g.num_experts, g.experts_per_token, ws.idx,
+                  nullptr, ws.gates, s);
+    }
+    if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
+    if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
+                                   reinterpret_cast<int32_t*>(gates_out), R, s);
+    run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
+                ws.idx, ws.gates, weights, static_cast<uint16_t*>(y), flags, ws, s);
+  });
+}
+
+size_t tfm_expert_routes_workspace_bytes(const tfm_plan* plan, int64_t n_routes) {
+  if (!plan || n_routes < 0) return 0;
+  const tfm_geometry& g = plan->g;
+  Carver c(nullptr);
+  c.take<WsHeader>(1);
+  c.take<int32_t>((size_t)n_routes);           // order
+  c.take<int32_t>((size_t)g.num_experts + 1);  // offsets
+  c.take<int32_t>((size_t)g.num_experts + 1);  // active
+  c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
+  c.take<float>((size_t)(n_routes * g.hidden_size));
+  return align_up(c.offset, 256);
+}
+
+int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
+                      const int32_t* token_indices, const int32_t* expert_ids, int64_t n_routes,
+                      int32_t experts_sorted, const tfm_moe_weights* weights, void* out_sorted,
+                      int32_t* inverse, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)experts_sorted;
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX, "tokens out of range");
+    need(n_routes >= 0 && n_routes <= INT32_MAX, "n_routes out of range");
+    const tfm_geometry& g = plan->g;
+    const size_t want = tfm_expert_routes_workspace_bytes(plan, n_routes);
+    need_ws(workspace, workspace_bytes, want);
+    if (n_routes == 0) return;
+    need_ptr(x, "x");
+    need_ptr(token_indices, "token_indices");
+    need_ptr(expert_ids, "expert_ids");
+    need_ptr(out_sorted, "out_sorted");
+    need_ptr(inverse, "inverse");
+    need_align16(x, "x");
+    check_weights(weights, false);
+    Carver c(workspace);
+    WsHeader* hdr = c.take<WsHeader>(1);
+    Grouping grp{};
+    grp.order = c.take<int32_t>((size_t)n_routes);
+    grp.offsets = c.take<int32_t>((size_t)g.num_experts + 1);
+    grp.active = c.take<int32_t>((size_t)g.num_experts + 1);
+    grp.inverse = inverse;
+    grp.E = g.num_experts;
+    uint16_t* h = c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
+    float* P = c.take<float>((size_t)(n_routes * g.hidden_size));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts;
+    launch_group(expert_ids, n_routes, E, grp, &hdr->status, s);
+    const RowMap rm{grp.order, token_indices, 1, tokens, &hdr->status};
+    const int max_active = (int)(n_routes < E ? n_routes : E);
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    if (n_routes <= plan->gemv_max_routes) {
+      launch_gemv_gateup(xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
+      launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
+    } else {
+      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, h, nullptr, 0, s);
+      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, nullptr, 1, nullptr, P, s);
+    }
+    launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
+  });
+}
+
+int tfm_profiler_create(int32_t capacity, tfm_profiler** out) {
+  return guarded([&] {
+    need_ptr(out, "out");
+    *out = nullptr;
+    need(capacity > 0 && capacity <= (1 << 20), "capacity must be in [1, 2^20]");
+    tfm_profiler* p = new tfm_profiler{};
+    p->capacity = capacity;
+    p->start.assign((size_t)capacity, nullptr);
+    p->end.assign((size_t)capacity, nullptr);
+    p->stage.assign((size_t)capacity, -1);
+    for (int i = 0; i < capacity; ++i) {
+      hipError_t a = hipEventCreate(&p->start[i]);
+      hipError_t b = a == hipSuccess ? hipEventCreate(&p->end[i]) : a;
+      if (b != hipSuccess) {
+        tfm_profiler_destroy(p);
+        check_hip(b, "hipEventCreate");
+      }
+    }
+    *out = p;
+  });
+}
+
+void tfm_profiler_destroy(tfm_profiler* p) {
+  if (!p) return;
+  if (g_profiler == p) g_profiler = nullptr;
+  for (hipEvent_t e : p->start)
+    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : p->end)
+    if (e) (void)hipEventDestroy(e);
+  delete p;
+}
+
+int tfm_profiler_attach(tfm_profiler* p) {
+  g_profiler = p;
+  return TFM_OK;
+}
+
+int tfm_profiler_reset(tfm_profiler* p) {
+  return guarded([&] {
+    need_ptr(p, "profiler");
+    p->used = 0;
+    p->dropped = 0;
+  });
+}
+
+int tfm_profiler_stage(tfm_profiler* p, int32_t stage, double* total_ms, int32_t* launches,
+                       int32_t* dropped) {
+  return guarded([&] {
+    need_ptr(p, "profiler");
+    need(stage >= 0 && stage < TFM_STAGE_COUNT, "unknown stage");
+    double sum = 0.0;
+    int n = 0;
+    for (int i = 0; i < p->used; ++i) {
+      if (p->stage[i] != stage) continue;
+      check_hip(hipEventSynchronize(p->end[i]), "hipEventSynchronize");
+      float ms = 0.0f;
+      check_hip(hipEventElapsedTime(&ms, p->start[i], p->end[i]), "hipEventElapsedTime");
+      sum += ms;
+      ++n;
+    }
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = n;
+    if (dropped) *dropped = p->dropped;
+  });
+}
+
+const char* tfm_stage_name(int32_t stage) {
+  static const char* names[TFM_STAGE_COUNT] = {"router", "topk", "group", "gateup", "down", "combine"};
+  return stage >= 0 && stage < TFM_STAGE_COUNT ? names[stage] : "";
+}
+
+int tfm_status_word(void* workspace, void* stream, uint32_t* status_out) {
+  return guarded([&] {
+    need_ptr(workspace, "workspace");
+    need_ptr(status_out, "status_out");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    WsHeader* hdr = static_cast<WsHeader*>(workspace);
+    uint32_t v = 0;
+    check_hip(hipMemcpyAsync(&v, &hdr->status, sizeof(v), hipMemcpyDeviceToHost, s), "status read");
+    check_hip(hipStreamSynchronize(s), "status sync");
+    const uint32_t zero = 0;
+    check_hip(hipMemcpyAsync(&hdr->status, &zero, sizeof(zero), hipMemcpyHostToDevice, s), "status clear");
+    check_hip(hipStreamSynchronize(s), "status sync");
+    *status_out = v;
+  });
+}
+
+}  // extern "C"

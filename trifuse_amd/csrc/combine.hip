@@ -1,0 +1,142 @@
+// Weighted combine and small elementwise kernels.
+//
+// The reference combines the K expert outputs of a token with the routing
+// gates and adds the residual (MLXNativeGraniteMoEPrefill.h:688-701, kernel
+// text :54-70). Here the down projection already multiplied each route's
+// output by its gate; the K rows are summed in k order in fp32, scaled by the
+// residual multiplier, added to the residual and rounded once to bf16.
+#include "tfm_device.h"
+#include "tfm_internal.h"
+
+namespace tfm {
+
+// 8 columns per thread; H % 8 == 0.
+__global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __restrict__ P,
+                                                             const int32_t* __restrict__ inverse,
+                                                             const int32_t* __restrict__ n_valid,
+                                                             int T, int K, int H,
+                                                             const uint16_t* __restrict__ residual,
+                                                             float rmul, uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = H / 8;
+  if (i >= (int64_t)T * per_row) return;
+  const int t = (int)(i / per_row), c = (int)(i % per_row) * 8;
+  float s[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) s[v] = 0.0f;
+  const int nv = *n_valid;
+  for (int k = 0; k < K; ++k) {
+    const int64_t row = inverse[(int64_t)t * K + k];
+    if (row >= nv) continue;
+    const float4* p = reinterpret_cast<const float4*>(P + row * H + c);
+    const float4 a = p[0], b = p[1];
+    s[0] += a.x; s[1] += a.y; s[2] += a.z; s[3] += a.w;
+    s[4] += b.x; s[5] += b.y; s[6] += b.z; s[7] += b.w;
+  }
+  float r[8];
+  if (residual) {
+    const uint4 rv = *reinterpret_cast<const uint4*>(residual + (int64_t)t * H + c);
+    r[0] = lo_bf(rv.x); r[1] = hi_bf(rv.x); r[2] = lo_bf(rv.y); r[3] = hi_bf(rv.y);
+    r[4] = lo_bf(rv.z); r[5] = hi_bf(rv.z); r[6] = lo_bf(rv.w); r[7] = hi_bf(rv.w);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) r[v] = 0.0f;
+  }
+  uint4 o;
+  o.x = pack_bf16x2(r[0] + rmul * s[0], r[1] + rmul * s[1]);
+  o.y = pack_bf16x2(r[2] + rmul * s[2], r[3] + rmul * s[3]);
+  o.z = pack_bf16x2(r[4] + rmul * s[4], r[5] + rmul * s[5]);
+  o.w = pack_bf16x2(r[6] + rmul * s[6], r[7] + rmul * s[7]);
+  *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
+}
+
+void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
+                           int K, int H, const uint16_t* residual, float rmul, uint16_t* y,
+                           hipStream_t s) {
+  if (T <= 0) return;
+  const int64_t n = (int64_t)T * (H / 8);
+  combine_sorted_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, inverse, n_valid, T, K, H,
+                                                                   residual, rmul, y);
+  check_hip(hipGetLastError(), "combine launch");
+}
+
+__global__ __launch_bounds__(256) void finalize_acc_kernel(const float* __restrict__ acc, int T,
+                                                           int H, const uint16_t* __restrict__ residual,
+                                                           float rmul, uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T * H / 8) return;
+  const int64_t base = i * 8;
+  const float4* p = reinterpret_cast<const float4*>(acc + base);
+  const float4 a = p[0], b = p[1];
+  const float s[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (residual) {
+    const uint4 rv = *reinterpret_cast<const uint4*>(residual + base);
+    r[0] = lo_bf(rv.x); r[1] = hi_bf(rv.x); r[2] = lo_bf(rv.y); r[3] = hi_bf(rv.y);
+    r[4] = lo_bf(rv.z); r[5] = hi_bf(rv.z); r[6] = lo_bf(rv.w); r[7] = hi_bf(rv.w);
+  }
+  uint4 o;
+  o.x = pack_bf16x2(r[0] + rmul * s[0], r[1] + rmul * s[1]);
+  o.y = pack_bf16x2(r[2] + rmul * s[2], r[3] + rmul * s[3]);
+  o.z = pack_bf16x2(r[4] + rmul * s[4], r[5] + rmul * s[5]);
+  o.w = pack_bf16x2(r[6] + rmul * s[6], r[7] + rmul * s[7]);
+  *reinterpret_cast<uint4*>(y + base) = o;
+}
+
+void launch_finalize_acc(const float* acc, int T, int H, const uint16_t* residual, float rmul,
+                         uint16_t* y, hipStream_t s) {
+  if (T <= 0) return;
+  const int64_t n = (int64_t)T * H / 8;
+  finalize_acc_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(acc, T, H, residual, rmul, y);
+  check_hip(hipGetLastError(), "finalize launch");
+}
+
+__global__ void rows_to_bf16_kernel(const float* __restrict__ P, int64_t n, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f2bf(P[i]);
+}
+
+void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s) {
+  const int64_t n = rows * H;
+  if (n <= 0) return;
+  rows_to_bf16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, n, out);
+  check_hip(hipGetLastError(), "rows_to_bf16 launch");
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+void launch_fill_f32(float* p, int64_t n, float v, hipStream_t s) {
+  if (n <= 0) return;
+  fill_f32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, v);
+  check_hip(hipGetLastError(), "fill launch");
+}
+
+__global__ void copy_i32_kernel(const int32_t* __restrict__ a, int32_t* __restrict__ b, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) b[i] = a[i];
+}
+
+void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return;
+  copy_i32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, dst, n);
+  check_hip(hipGetLastError(), "copy launch");
+}
+
+__global__ void gates_to_f32_kernel(int from_bf16, const void* __restrict__ src,
+                                    float* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = from_bf16 ? bf2f(static_cast<const uint16_t*>(src)[i]) : static_cast<const float*>(src)[i];
+}
+
+void launch_gates_to_f32(int dtype_native_bf16, const void* src, float* dst, int64_t n,
+                         hipStream_t s) {
+  if (n <= 0) return;
+  gates_to_f32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dtype_native_bf16, src, dst, n);
+  check_hip(hipGetLastError(), "gates launch");
+}
+
+}  // namespace tfm

@@ -1,0 +1,287 @@
+// Router linear, OLMoE/Granite routing and the OLMoE softmax.
+//
+// Bit-defined arithmetic (the routing must reproduce exactly):
+//  * logits[t,e] = bf16(tree64(s_0..s_63) [+ bias[e]]), lane l summing
+//    x*w over h in [l*c, l*c+c) (c = H/64) with sequential fmaf from 0, and
+//    tree64 the natural pairwise tree over lanes (l^1 first, then l^2, ...).
+//  * softmax: max by compare-select from -FLT_MAX (NaN skipped), e = exp(l-max)
+//    with route_expf, normaliser = 1/(tree over four-value chunks, each chunk
+//    summed in order), p = e * normaliser (MLXOLMoERouter.h:26-61).
+//  * ranks as in MLXOLMoERouter.h:65-83 (OLMoE) and
+//    MLXNativeGraniteMoEPrefill.h:92-109 (Granite).
+#include "tfm_device.h"
+#include "tfm_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace tfm {
+
+// One wave per (token tile of TW tokens, expert tile of EPW experts).
+template <int C, int TW>
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const float* __restrict__ bias,
+                                                            int T, int H, int E, int EPW,
+                                                            uint16_t* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n_tt = (T + TW - 1) / TW;
+  const int n_et = (E + EPW - 1) / EPW;
+  if (wave >= n_tt * n_et) return;
+  const int tt = wave % n_tt, et = wave / n_tt;
+  float xv[TW][C];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int tok = tt * TW + t;
+    if (tok < T) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + (int64_t)tok * H + lane * C);
+#pragma unroll
+      for (int i = 0; i < C / 8; ++i) {
+        const uint4 v = src[i];
+        xv[t][8 * i + 0] = lo_bf(v.x); xv[t][8 * i + 1] = hi_bf(v.x);
+        xv[t][8 * i + 2] = lo_bf(v.y); xv[t][8 * i + 3] = hi_bf(v.y);
+        xv[t][8 * i + 4] = lo_bf(v.z); xv[t][8 * i + 5] = hi_bf(v.z);
+        xv[t][8 * i + 6] = lo_bf(v.w); xv[t][8 * i + 7] = hi_bf(v.w);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C; ++j) xv[t][j] = 0.0f;
+    }
+  }
+  const int e_end = min(E, (et + 1) * EPW);
+  for (int e = et * EPW; e < e_end; ++e) {
+    float wv[C];
+    const uint4* src = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 8; ++i) {
+      const uint4 v = src[i];
+      wv[8 * i + 0] = lo_bf(v.x); wv[8 * i + 1] = hi_bf(v.x);
+      wv[8 * i + 2] = lo_bf(v.y); wv[8 * i + 3] = hi_bf(v.y);
+      wv[8 * i + 4] = lo_bf(v.z); wv[8 * i + 5] = hi_bf(v.z);
+      wv[8 * i + 6] = lo_bf(v.w); wv[8 * i + 7] = hi_bf(v.w);
+    }
+    const float be = bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
+      s = group_sum<64>(s);
+      const int tok = tt * TW + t;
+      if (lane == 0 && tok < T) {
+        const float v = bias ? s + be : s;
+        logits[(int64_t)tok * E + e] = f2bf(v);
+      }
+    }
+  }
+}
+
+// Any H % 64 == 0: the same arithmetic with scalar loads.
+__global__ __launch_bounds__(256) void router_logits_generic(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             int T, int H, int E,
+                                                             uint16_t* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= T * E) return;
+  const int tok = wave / E, e = wave % E;
+  const int c = H / 64;
+  float s = 0.0f;
+  for (int j = 0; j < c; ++j)
+    s = __builtin_fmaf(bf2f(x[(int64_t)tok * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
+  s = group_sum<64>(s);
+  if (lane == 0) logits[(int64_t)tok * E + e] = f2bf(bias ? s + bias[e] : s);
+}
+
+template <int C>
+static void launch_router_c(const uint16_t* x, const uint16_t* w, const float* bias, int T,
+                            int H, int E, uint16_t* logits, hipStream_t s) {
+  if (T <= 64) {
+    // Few tokens: one wave per (token, expert), so the router rows stream in
+    // parallel across the chip.
+    const int waves = T * E;
+    router_logits_kernel<C, 1><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, 1, logits);
+  } else {
+    // Many tokens: a wave keeps 4 token rows in registers and walks 16
+    // experts, reading router rows from L2.
+    constexpr int TW = 4;
+    const int EPW = 16;
+    const int waves = ((T + TW - 1) / TW) * ((E + EPW - 1) / EPW);
+    router_logits_kernel<C, TW><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, EPW, logits);
+  }
+}
+
+void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int T,
+                          int H, int E, uint16_t* logits, hipStream_t s) {
+  if (T <= 0) return;
+  switch (H) {
+    case 512: launch_router_c<8>(x, w, bias, T, H, E, logits, s); break;
+    case 1024: launch_router_c<16>(x, w, bias, T, H, E, logits, s); break;
+    case 1536: launch_router_c<24>(x, w, bias, T, H, E, logits, s); break;
+    case 2048: launch_router_c<32>(x, w, bias, T, H, E, logits, s); break;
+    default: {
+      const int64_t waves = (int64_t)T * E;
+      router_logits_generic<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(x, w, bias, T, H, E, logits);
+    }
+  }
+  check_hip(hipGetLastError(), "router_logits launch");
+}
+
+// Softmax over 64 lanes (absent lanes hold -inf): returns e_l and writes the
+// normaliser 1/sum, all in the bit-defined order described at the top.
+__device__ __forceinline__ float wave_softmax_exp(float ld, float* norm) {
+  float m = -3.40282347e38f;
+  m = m < ld ? ld : m;
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) m = fmaxf(m, shfl_xor_f(m, k));
+  const float ex = route_expf(ld - m);
+  const int lane = threadIdx.x & 63;
+  const int q0 = lane & ~3;
+  const float a0 = shfl_f(ex, q0), a1 = shfl_f(ex, q0 + 1), a2 = shfl_f(ex, q0 + 2),
+              a3 = shfl_f(ex, q0 + 3);
+  float s = a0 + a1;
+  s = s + a2;
+  s = s + a3;
+  s = s + shfl_xor_f(s, 4);
+  s = s + shfl_xor_f(s, 8);
+  s = s + shfl_xor_f(s, 16);
+  s = s + shfl_xor_f(s, 32);
+  *norm = 1.0f / s;
+  return ex;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// One wave per token. gates_native: bf16 probabilities (OLMoE) or fp32
+// (Granite); gates_f32: fp32 copy. Either may be null.
+template <int ROUTE>
+__global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ logits, int T,
+                                                   int E, int K, int32_t* __restrict__ idx,
+                                                   void* __restrict__ gates_native,
+                                                   float* __restrict__ gates_f32) {
+  __shared__ float sel[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wv;
+  const bool live = t < T;
+  const bool valid = live && lane < E;
+  const uint16_t raw = valid ? logits[(int64_t)t * E + lane] : (uint16_t)0;
+  if (ROUTE == TFM_ROUTE_OLMOE) {
+    const float ld = valid ? bf2f(raw) : -__builtin_inff();
+    float norm;
+    const float ex = wave_softmax_exp(ld, &norm);
+    const uint16_t pb = f2bf(ex * norm);
+    const float p = bf2f(pb);
+    const bool pn = p != p;
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+      const float o = readlane_f(p, j);
+      const bool on = o != o;
+      const bool before = !on && (pn || o > p);
+      const bool equal = (on && pn) || (!on && !pn && o == p);
+      rank += (before || (equal && j < lane)) ? 1 : 0;
+    }
+    if (valid && rank < K) {
+      idx[(int64_t)t * K + rank] = lane;
+      if (gates_native) static_cast<uint16_t*>(gates_native)[(int64_t)t * K + rank] = pb;
+      if (gates_f32) gates_f32[(int64_t)t * K + rank] = p;
+    }
+  } else {
+    const float v = bf2f(raw);
+    const bool vn = v != v;
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+      const float o = readlane_f(v, j);
+      const bool on = o != o;
+      const bool less = !on && (vn || o < v);
+      const bool equal = (on && vn) || (!on && !vn && o == v);
+      rank += (less || (equal && j < lane)) ? 1 : 0;
+    }
+    if (valid && rank >= E - K) {
+      const int slot = rank - (E - K);
+      sel[wv][slot] = v;
+      idx[(int64_t)t * K + slot] = lane;
+    }
+    __syncthreads();
+    const float ld = (live && lane < K) ? sel[wv][lane] : -__builtin_inff();
+    float norm;
+    const float ex = wave_softmax_exp(ld, &norm);
+    const float g = ex * norm;
+    if (live && lane < K) {
+      if (gates_native) static_cast<float*>(gates_native)[(int64_t)t * K + lane] = g;
+      if (gates_f32) gates_f32[(int64_t)t * K + lane] = g;
+    }
+  }
+}
+
+void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                 void* gates_native, float* gates_f32, hipStream_t s) {
+  if (T <= 0) return;
+  const unsigned blocks = (unsigned)((T + 3) / 4);
+  if (route_kind == TFM_ROUTE_OLMOE)
+    topk_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
+  else
+    topk_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
+  check_hip(hipGetLastError(), "topk launch");
+}
+
+// Ranking only (values given): one wave per row.
+template <int RULE>
+__global__ __launch_bounds__(256) void rank_topk_kernel(const uint16_t* __restrict__ values, int T,
+                                                        int n, int K, int32_t* __restrict__ idx) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave exits together
+  const bool valid = lane < n;
+  const float v = valid ? bf2f(values[(int64_t)t * n + lane]) : 0.0f;
+  const bool vn = v != v;
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const float o = readlane_f(v, j);
+    const bool on = o != o;
+    const bool equal = (on && vn) || (!on && !vn && o == v);
+    const bool ahead = RULE == TFM_ROUTE_OLMOE ? (!on && (vn || o > v)) : (!on && (vn || o < v));
+    rank += (ahead || (equal && j < lane)) ? 1 : 0;
+  }
+  if (!valid) return;
+  if (RULE == TFM_ROUTE_OLMOE) {
+    if (rank < K) idx[(int64_t)t * K + rank] = lane;
+  } else {
+    if (rank >= n - K) idx[(int64_t)t * K + rank - (n - K)] = lane;
+  }
+}
+
+void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
+                      hipStream_t s) {
+  if (T <= 0) return;
+  const unsigned blocks = (unsigned)((T + 3) / 4);
+  if (rule == TFM_ROUTE_OLMOE)
+    rank_topk_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+  else
+    rank_topk_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+  check_hip(hipGetLastError(), "rank_topk launch");
+}
+
+__global__ __launch_bounds__(256) void olmoe_softmax_kernel(const uint16_t* __restrict__ logits,
+                                                            int T, int E,
+                                                            uint16_t* __restrict__ probs) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave exits together
+  const bool valid = lane < E;
+  const float ld = valid ? bf2f(logits[(int64_t)t * E + lane]) : -__builtin_inff();
+  float norm;
+  const float ex = wave_softmax_exp(ld, &norm);
+  if (valid) probs[(int64_t)t * E + lane] = f2bf(ex * norm);
+}
+
+void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s) {
+  if (T <= 0) return;
+  olmoe_softmax_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(logits, T, E, probs);
+  check_hip(hipGetLastError(), "olmoe_softmax launch");
+}
+
+}  // namespace tfm

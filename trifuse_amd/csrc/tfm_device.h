@@ -1,0 +1,105 @@
+// Device-side helpers shared by the MoE kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tfm {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round to nearest even, NaN kept quiet with its sign. Integer arithmetic, so
+// the result does not depend on the hardware denormal mode.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Two floats to packed bf16 (low = a), hardware round-to-nearest-even.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Unpack the low/high bf16 of a 32-bit word to float.
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// exp for the routing softmax. Cody-Waite reduction x = n*ln2 + r with
+// ln2 = 0x1.62e4p-1 + 0x1.7f7d1cp-20, then the degree-7 Taylor polynomial of
+// e^r (coefficients fl(1/k!)) by Horner with fused multiply-adds, scaled by
+// 2^n. x < -80 gives 0 so that softmax terms never become subnormal.
+__device__ __forceinline__ float route_expf(float x) {
+  if (x != x) return x;
+  if (x < -80.0f) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  const float n = __builtin_rintf(x * 0x1.715476p+0f);
+  float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+  r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, kWave); }
+
+// Sum over aligned groups of G lanes (G a power of two <= 64). The tree is
+// the natural pairwise one: lanes l and l^1 first, then pairs of pairs.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < G; m <<= 1) v = v + shfl_xor_f(v, m);
+  return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+// 8 nibbles of a packed word (LSB first) dequantised as s*q+b, as floats.
+// q order: element i is bits [4i, 4i+4).
+__device__ __forceinline__ void dequant8(uint32_t w, float s, float b, float* out) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  out[0] = __builtin_fmaf(s, (float)(lo & 0xffu), b);
+  out[1] = __builtin_fmaf(s, (float)(hi & 0xffu), b);
+  out[2] = __builtin_fmaf(s, (float)((lo >> 8) & 0xffu), b);
+  out[3] = __builtin_fmaf(s, (float)((hi >> 8) & 0xffu), b);
+  out[4] = __builtin_fmaf(s, (float)((lo >> 16) & 0xffu), b);
+  out[5] = __builtin_fmaf(s, (float)((hi >> 16) & 0xffu), b);
+  out[6] = __builtin_fmaf(s, (float)(lo >> 24), b);
+  out[7] = __builtin_fmaf(s, (float)(hi >> 24), b);
+}
+
+// Sum_i q_i * x_i over the 8 nibbles of a packed word (x in element order).
+__device__ __forceinline__ float qdot8(uint32_t w, const float* x, float acc) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  acc = __builtin_fmaf((float)(lo & 0xffu), x[0], acc);
+  acc = __builtin_fmaf((float)(hi & 0xffu), x[1], acc);
+  acc = __builtin_fmaf((float)((lo >> 8) & 0xffu), x[2], acc);
+  acc = __builtin_fmaf((float)((hi >> 8) & 0xffu), x[3], acc);
+  acc = __builtin_fmaf((float)((lo >> 16) & 0xffu), x[4], acc);
+  acc = __builtin_fmaf((float)((hi >> 16) & 0xffu), x[5], acc);
+  acc = __builtin_fmaf((float)(lo >> 24), x[6], acc);
+  acc = __builtin_fmaf((float)(hi >> 24), x[7], acc);
+  return acc;
+}
+
+}  // namespace tfm

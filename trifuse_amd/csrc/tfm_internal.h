@@ -1,0 +1,130 @@
+// Internal host-side declarations shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/trifuse_moe.h"
+
+namespace tfm {
+
+// Status reporting: every entry point catches tfm::Error and returns its code.
+struct Error {
+  int code;
+  std::string message;
+};
+[[noreturn]] void fail(int code, const std::string& message);
+void check_hip(hipError_t err, const char* what);
+void set_last_error(const std::string& message);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Workspace carve-up: regions are 256-byte aligned, in declaration order.
+struct Carver {
+  char* base;
+  size_t offset = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    offset = align_up(offset, 256);
+    T* p = base ? reinterpret_cast<T*>(base + offset) : nullptr;
+    offset += count * sizeof(T);
+    return p;
+  }
+};
+
+// Header at the start of every workspace.
+struct WsHeader {
+  uint32_t status;   // TFM_STATUS_* bits, sticky until tfm_status_word reads them
+  uint32_t pad[63];
+};
+
+// Grouping results shared by every consumer of a route list.
+struct Grouping {
+  int32_t* order;    // [n] sorted position -> flat route
+  int32_t* inverse;  // [n] flat route -> sorted position
+  int32_t* offsets;  // [E+1]
+  int32_t* active;   // [E+1] ids of experts with routes, ascending; active[E] = count
+  int E;             // number of experts
+};
+
+// ---- launchers (defined in the .hip files) ----
+void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int T,
+                          int H, int E, uint16_t* logits, hipStream_t s);
+void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                 void* gates_native, float* gates_f32, hipStream_t s);
+void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
+                      hipStream_t s);
+void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
+void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, uint32_t* status,
+                  hipStream_t s);
+
+// Row source of a sorted route j: x row = x_rows ? x_rows[order[j]] : order[j] / K.
+// Rows outside [0, nx) are read as row 0 and flag TFM_STATUS_BAD_ROW_INDEX.
+struct RowMap {
+  const int32_t* order;
+  const int32_t* x_rows;  // may be null
+  int K;                  // used when x_rows is null
+  int64_t nx;             // rows of x
+  uint32_t* status;       // workspace status word
+};
+
+__device__ __forceinline__ int64_t route_row(const RowMap& rm, int j) {
+  const int f = rm.order[j];
+  int64_t r = rm.x_rows ? (int64_t)rm.x_rows[f] : (int64_t)(f / rm.K);
+  if (r < 0 || r >= rm.nx) {
+    atomicOr(rm.status, (uint32_t)TFM_STATUS_BAD_ROW_INDEX);
+    r = 0;
+  }
+  return r;
+}
+
+// Decode-style (few routes per expert) dequant GEMV family.
+//   gateup: h[j, n] = bf16(silu(xg) * xu)            (sorted route j)
+//   plain:  out[order[j], n] = bf16(x . w)            (gather_qmm)
+//   scaled: P[j, n] = (x . w) * gate[order[j]]        (fp32, down + combine)
+// `routes` is the total route count (sizes the per-pass route batch).
+void launch_gemv_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+                        int64_t routes, const tfm_affine& gate, const tfm_affine& up, int N,
+                        int Kin, uint16_t* h, hipStream_t s);
+void launch_gemv_plain(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+                       int64_t routes, const tfm_affine& w, int N, int Kin, uint16_t* out,
+                       hipStream_t s);
+void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_active,
+                        int64_t routes, const tfm_affine& w, int N, int Kin, const float* gates,
+                        float* P, hipStream_t s);
+
+// Prefill-style grouped GEMM (dequant to LDS bf16, MFMA).
+//   gateup: h[j, :] = bf16(silu(x W_gate^T) * (x W_up^T)) for sorted routes j
+//   down:   acc[tok(j), :] += gate_j * (h[j, :] W_down^T)   (fp32 atomics), or
+//           P[j, :] = gate_j * (h[j, :] W_down^T)           (deterministic)
+//   plain:  out[order[j], :] = bf16(x W^T)                  (gather_qmm)
+void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
+                         int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
+                         uint16_t* h, float* zero_buf, int64_t zero_count, hipStream_t s);
+void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
+                       const tfm_affine& w, int N, int Kin, const float* gates, int K,
+                       float* acc, float* P, hipStream_t s);
+void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
+                        int E, const tfm_affine& w, int N, int Kin, uint16_t* out,
+                        hipStream_t s);
+
+// Combine: y[t, c] = bf16(residual[t, c] + rm * sum_k P[inverse[t*K+k], c]) (k ascending)
+// Routes whose sorted position is >= *n_valid (bad expert ids) contribute 0.
+void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
+                           int K, int H, const uint16_t* residual, float rmul, uint16_t* y,
+                           hipStream_t s);
+// Finalize: y[t, c] = bf16(residual[t, c] + rm * acc[t, c])
+void launch_finalize_acc(const float* acc, int T, int H, const uint16_t* residual, float rmul,
+                         uint16_t* y, hipStream_t s);
+// Expert-sorted output rows for the hook: out[j, c] = bf16(P[j, c])
+void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s);
+void launch_fill_f32(float* p, int64_t n, float v, hipStream_t s);
+void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s);
+void launch_gates_to_f32(int dtype_native_bf16, const void* src, float* dst, int64_t n,
+                         hipStream_t s);
+
+}  // namespace tfm
