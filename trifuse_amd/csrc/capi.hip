@@ -139,6 +139,13 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   return w;
 }
 
+// The decode path (routing per token, grouping in the gate/up prologue)
+// applies when every route fits one grouping thread and both matmul widths
+// fit one 32-element chunk per lane.
+static bool fused_decode(const tfm_geometry& g, int64_t R) {
+  return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
+}
+
 struct GroupWs {
   WsHeader* hdr;
   Grouping grp;
@@ -202,13 +209,14 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const tfm_geometry& g = p->g;
   const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
   const int64_t R = T * K;
+  const bool gemv = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
   {
     StageScope st(TFM_STAGE_GROUP, s);
     launch_group(idx, R, E, ws.grp, &ws.hdr->status, s);
   }
   const int max_active = (int)(R < E ? R : E);
   const RowMap rm{ws.grp.order, nullptr, K, T, &ws.hdr->status};
-  if (R <= p->gemv_max_routes) {
+  if (gemv) {
     {
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_gemv_gateup(x, rm, ws.grp, max_active, R, w->gate, w->up, I, H, ws.h, s);
@@ -429,7 +437,7 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
     const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
     const int max_active = (int)(rows < num_experts ? rows : num_experts);
-    if (rows <= gemv_threshold())
+    if (rows <= gemv_threshold() && k_in <= 2048)
       launch_gemv_plain(static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
                         static_cast<uint16_t*>(out), s);
     else
@@ -479,6 +487,36 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
     need_ws(workspace, workspace_bytes, ws.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t R = tokens * g.experts_per_token;
+    const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
+    const int H = g.hidden_size, I = g.intermediate_size;
+    if (fused_decode(g, R)) {
+      {
+        StageScope st(TFM_STAGE_ROUTER, s);
+        launch_decode_route(g.route, static_cast<const uint16_t*>(x),
+                            static_cast<const uint16_t*>(weights->router), weights->logit_bias, T,
+                            H, E, K, nullptr, ws.idx, ws.gates, s);
+      }
+      {
+        StageScope st(TFM_STAGE_GATEUP, s);
+        launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, T, E, K, H, I, weights->gate,
+                             weights->up, ws.grp, ws.h, &ws.hdr->status, s);
+      }
+      const int max_active = (int)(R < E ? R : E);
+      {
+        StageScope st(TFM_STAGE_DOWN, s);
+        launch_gemv_scaled(ws.h, ws.grp, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
+      }
+      {
+        StageScope st(TFM_STAGE_COMBINE, s);
+        launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
+                              static_cast<const uint16_t*>(residual), g.residual_multiplier,
+                              static_cast<uint16_t*>(y), s);
+      }
+      if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
+      if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
+                                     reinterpret_cast<int32_t*>(gates_out), R, s);
+      return;
+    }
     {
       StageScope st(TFM_STAGE_ROUTER, s);
       launch_router_logits(static_cast<const uint16_t*>(x),
@@ -547,7 +585,7 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     const RowMap rm{grp.order, token_indices, 1, tokens, &hdr->status};
     const int max_active = (int)(n_routes < E ? n_routes : E);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
-    if (n_routes <= plan->gemv_max_routes) {
+    if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048) {
       launch_gemv_gateup(xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
       launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
     } else {

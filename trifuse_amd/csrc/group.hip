@@ -23,13 +23,16 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t* __r
                                                               int32_t* __restrict__ inverse,
                                                               int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ active,
-                                                              uint32_t* __restrict__ status) {
+                                                              uint32_t* __restrict__ status,
+                                                              uint32_t* __restrict__ zero,
+                                                              int zero_words) {
   __shared__ int hist[kMaxBuckets];
   __shared__ int run[kMaxBuckets];
   __shared__ int wave_cnt[kGroupWaves][kMaxBuckets];
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int B = E + 1;  // bucket E collects out-of-range ids
+  for (int i = tid; i < zero_words; i += kGroupThreads) zero[i] = 0u;
   for (int i = tid; i < B; i += kGroupThreads) hist[i] = 0;
   for (int i = tid; i < kGroupWaves * kMaxBuckets; i += kGroupThreads) (&wave_cnt[0][0])[i] = 0;
   __syncthreads();
@@ -97,9 +100,9 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t* __r
 }
 
 void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, uint32_t* status,
-                  hipStream_t s) {
+                  hipStream_t s, uint32_t* zero, int zero_words) {
   group_kernel<<<1, kGroupThreads, 0, s>>>(ids, n, E, g.order, g.inverse, g.offsets, g.active,
-                                           status);
+                                           status, zero, zero_words);
   check_hip(hipGetLastError(), "group launch");
 }
 

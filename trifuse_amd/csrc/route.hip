@@ -9,6 +9,7 @@
 //    summed in order), p = e * normaliser (MLXOLMoERouter.h:26-61).
 //  * ranks as in MLXOLMoERouter.h:65-83 (OLMoE) and
 //    MLXNativeGraniteMoEPrefill.h:92-109 (Granite).
+#include "route_wave.h"
 #include "tfm_device.h"
 #include "tfm_internal.h"
 
@@ -128,29 +129,6 @@ void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bia
   check_hip(hipGetLastError(), "router_logits launch");
 }
 
-// Softmax over 64 lanes (absent lanes hold -inf): returns e_l and writes the
-// normaliser 1/sum, all in the bit-defined order described at the top.
-__device__ __forceinline__ float wave_softmax_exp(float ld, float* norm) {
-  float m = -3.40282347e38f;
-  m = m < ld ? ld : m;
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) m = fmaxf(m, shfl_xor_f(m, k));
-  const float ex = route_expf(ld - m);
-  const int lane = threadIdx.x & 63;
-  const int q0 = lane & ~3;
-  const float a0 = shfl_f(ex, q0), a1 = shfl_f(ex, q0 + 1), a2 = shfl_f(ex, q0 + 2),
-              a3 = shfl_f(ex, q0 + 3);
-  float s = a0 + a1;
-  s = s + a2;
-  s = s + a3;
-  s = s + shfl_xor_f(s, 4);
-  s = s + shfl_xor_f(s, 8);
-  s = s + shfl_xor_f(s, 16);
-  s = s + shfl_xor_f(s, 32);
-  *norm = 1.0f / s;
-  return ex;
-}
-
 __device__ __forceinline__ float readlane_f(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
@@ -162,58 +140,23 @@ __global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ 
                                                    int E, int K, int32_t* __restrict__ idx,
                                                    void* __restrict__ gates_native,
                                                    float* __restrict__ gates_f32) {
-  __shared__ float sel[4][64];
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wv;
-  const bool live = t < T;
-  const bool valid = live && lane < E;
-  const uint16_t raw = valid ? logits[(int64_t)t * E + lane] : (uint16_t)0;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave exits together
+  const uint16_t* row = logits + (int64_t)t * E;
+  float g;
+  int id;
   if (ROUTE == TFM_ROUTE_OLMOE) {
-    const float ld = valid ? bf2f(raw) : -__builtin_inff();
-    float norm;
-    const float ex = wave_softmax_exp(ld, &norm);
-    const uint16_t pb = f2bf(ex * norm);
-    const float p = bf2f(pb);
-    const bool pn = p != p;
-    int rank = 0;
-    for (int j = 0; j < E; ++j) {
-      const float o = readlane_f(p, j);
-      const bool on = o != o;
-      const bool before = !on && (pn || o > p);
-      const bool equal = (on && pn) || (!on && !pn && o == p);
-      rank += (before || (equal && j < lane)) ? 1 : 0;
-    }
-    if (valid && rank < K) {
-      idx[(int64_t)t * K + rank] = lane;
-      if (gates_native) static_cast<uint16_t*>(gates_native)[(int64_t)t * K + rank] = pb;
-      if (gates_f32) gates_f32[(int64_t)t * K + rank] = p;
-    }
+    uint16_t gb;
+    id = olmoe_route_wave(row, E, K, &g, &gb);
+    if (lane < K && gates_native) static_cast<uint16_t*>(gates_native)[(int64_t)t * K + lane] = gb;
   } else {
-    const float v = bf2f(raw);
-    const bool vn = v != v;
-    int rank = 0;
-    for (int j = 0; j < E; ++j) {
-      const float o = readlane_f(v, j);
-      const bool on = o != o;
-      const bool less = !on && (vn || o < v);
-      const bool equal = (on && vn) || (!on && !vn && o == v);
-      rank += (less || (equal && j < lane)) ? 1 : 0;
-    }
-    if (valid && rank >= E - K) {
-      const int slot = rank - (E - K);
-      sel[wv][slot] = v;
-      idx[(int64_t)t * K + slot] = lane;
-    }
-    __syncthreads();
-    const float ld = (live && lane < K) ? sel[wv][lane] : -__builtin_inff();
-    float norm;
-    const float ex = wave_softmax_exp(ld, &norm);
-    const float g = ex * norm;
-    if (live && lane < K) {
-      if (gates_native) static_cast<float*>(gates_native)[(int64_t)t * K + lane] = g;
-      if (gates_f32) gates_f32[(int64_t)t * K + lane] = g;
-    }
+    id = granite_route_wave(row, E, K, &g);
+    if (lane < K && gates_native) static_cast<float*>(gates_native)[(int64_t)t * K + lane] = g;
+  }
+  if (lane < K) {
+    idx[(int64_t)t * K + lane] = id;
+    if (gates_f32) gates_f32[(int64_t)t * K + lane] = g;
   }
 }
 

@@ -59,8 +59,17 @@ void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, in
 void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
                       hipStream_t s);
 void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
+// Grouping; also zeroes `zero_words` words at `zero` (counters of a later kernel).
 void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, uint32_t* status,
-                  hipStream_t s);
+                  hipStream_t s, uint32_t* zero = nullptr, int zero_words = 0);
+
+// Decode path (decode.hip), T*K <= 256 routes.
+void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
+                         int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
+                         hipStream_t s);
+void launch_decode_gateup(const uint16_t* x, const int32_t* idx, int T, int E, int K, int H, int I,
+                          const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
+                          uint16_t* h, uint32_t* status, hipStream_t s);
 
 // Row source of a sorted route j: x row = x_rows ? x_rows[order[j]] : order[j] / K.
 // Rows outside [0, nx) are read as row 0 and flag TFM_STATUS_BAD_ROW_INDEX.
