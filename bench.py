@@ -8,7 +8,9 @@ weights and inputs resident in HBM:
   olmoe_decode_t8_x16 (default, the headline line): 8 tokens through 16
   independent OLMoE MoE layers (hidden 2048, 64 experts, top-8, intermediate
   1024, 4-bit affine g=64 experts, bf16 scales/biases).
-`value` is MoE-layer tok/s = tokens x layers / step time.
+`value` is MoE-layer tok/s = tokens x layers / step time. Every workload
+rotates through 16 distinct layers per step (16 layers exceed the 256 MB
+last-level cache), so per-layer latency is measured with weights from HBM.
 
 The other workloads (decode 1 token, prefill 512, prefill 4096 with Zipf
 routing, Granite prefill 2048 and decode 32) are measured in the same run and
@@ -84,7 +86,10 @@ class Runner:
         self.wl = wl.WORKLOADS[name]
         g = self.wl.geometry
         self.geom = g
-        self.layers = wl.workload_layers(self.wl, device)
+        # Rotate through TIMING_LAYERS distinct layers so weights come from HBM,
+        # not from the last-level cache (a single layer is 28-226 MB).
+        self.nlayers = max(self.wl.layers, wl.TIMING_LAYERS)
+        self.layers = wl.workload_layers(self.wl, device, self.nlayers)
         self.weights = [tmoe.ExpertWeights.from_layer(l) for l in self.layers]
         self.x = wl.workload_x(self.wl).to(device)
         self.block = tmoe.MoEBlock(g.hidden, g.intermediate, g.experts, g.top_k, route=g.route)
@@ -140,7 +145,7 @@ class Runner:
 def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages):
     from trifuse_amd import workload as wl
 
-    g, T, L = r.geom, r.wl.tokens, r.wl.layers
+    g, T, L = r.geom, r.wl.tokens, r.nlayers
     U = r.distinct_experts()
     per_layer_ms = ms_per_step / L
     bytes_step = sum(wl.algorithmic_bytes(g, T, u) for u in U)
@@ -150,7 +155,7 @@ def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages):
     bound = "hbm" if r.wl.name in DECODE else "mfma"
     rep = {
         "description": r.wl.description,
-        "tokens": T, "layers": L,
+        "tokens": T, "layers_per_step": L,
         "per_layer_us": per_layer_ms * 1e3,
         "tok_per_s": T * L / (ms_per_step * 1e-3),
         "wall_ms_per_step": wall_ms,
@@ -179,7 +184,7 @@ def dominant_roofline(r: Runner, stages):
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
         achieved = per_launch / dur_s / 1e9
-        return {"kernel": "gemv_kernel<gateup>", "bound": "hbm", "achieved": achieved,
+        return {"kernel": "decode_gateup_kernel", "bound": "hbm", "achieved": achieved,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                 "traffic": None, "alg_bytes_per_launch": per_launch,
                 "us_per_launch": st["us_per_launch"]}
@@ -188,6 +193,26 @@ def dominant_roofline(r: Runner, stages):
     return {"kernel": "ggemm_kernel<gateup>", "bound": "mfma", "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
             "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summaries (profiles/pmc_traffic_*.md), or None."""
+    import glob
+    import re
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    for path in sorted(glob.glob(os.path.join(here, "profiles", "pmc_traffic_*.md"))):
+        with open(path) as f:
+            text = f.read()
+        for block in re.findall(r"```json\n(.*?)\n```", text, re.S):
+            try:
+                d = json.loads(block)
+            except ValueError:
+                continue
+            if workload in d:
+                return d[workload].get("traffic_bytes")
+    return None
 
 
 def cpu_baseline(r: Runner, seconds: float):
@@ -210,7 +235,7 @@ def cpu_baseline(r: Runner, seconds: float):
     class NpLayer:
         pass
 
-    for lay in r.layers:
+    for lay in r.layers[:r.wl.layers]:
         nl = NpLayer()
         for name in ("gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q", "down_s", "down_b"):
             t = getattr(lay, name).cpu()
@@ -226,7 +251,7 @@ def cpu_baseline(r: Runner, seconds: float):
         if elapsed >= seconds:
             break
     return {"value": done_tokens / elapsed, "unit": "tok/s", "cores": used, "kind": "port",
-            "sample": f"{layers} of {r.wl.layers} layers x {T} tokens of {r.wl.name}, "
+            "sample": f"{layers} layer(s) x {T} tokens of {r.wl.name}, "
                       f"{elapsed:.1f} s, {used} OpenMP threads on {model}",
             "per_layer_ms": elapsed / layers * 1e3}
 
@@ -253,6 +278,7 @@ def main():
     stages = head.stage_times(max(10, min(args.steps, 100)))
     report = workload_report(head, ms, wall, stages)
     roof = dominant_roofline(head, stages)
+    roof["traffic"] = measured_traffic(args.workload)
 
     per = {args.workload: report}
     if not args.no_extra:
@@ -294,7 +320,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": args.workload, "hidden": g.hidden, "experts": g.experts,
                    "top_k": g.top_k, "intermediate": g.intermediate, "tokens": head.wl.tokens,
-                   "layers": head.wl.layers, "weights": "4-bit affine g64, bf16 scales/biases",
+                   "layers": head.nlayers, "weights": "4-bit affine g64, bf16 scales/biases",
                    "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -1,0 +1,283 @@
+"""Pins the CPU oracle (oracle/) on the host, independently of its own code.
+
+Each oracle function is checked against something it does not share code with:
+the reference's closed forms (native_affine_ops.py:29-36 dequantisation,
+the torch bodies of native_olmoe_topk_indices / native_topk_indices), exact
+special cases (one-hot router rows, bf16 rounding against torch), float64
+references within stated tolerances, brute force on tiny shapes, and planted
+mistakes (reversed nibble order, transposed weights, swapped gate/up, dropped
+bias, reversed tie rule) that must fail the same checks.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+RNG = np.random.default_rng(20261201)
+
+
+def bf(x):
+    return oracle.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def f(h):
+    return oracle.bf16_to_f32(h).astype(np.float64)
+
+
+# ---------------------------------------------------------------- bf16 / exp
+
+def test_bf16_round_nearest_even_matches_torch():
+    x = np.concatenate([
+        RNG.standard_normal(200000).astype(np.float32) * 10,
+        (RNG.random(50000).astype(np.float32) - 0.5) * 1e-30,
+        np.array([0.0, -0.0, 1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 3.4e38, -3.4e38, np.inf, -np.inf,
+                  1e-40, 2 ** -126], dtype=np.float32),
+    ])
+    ours = oracle.f32_to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)
+    assert oracle.f32_to_bf16(np.array([1 + 2 ** -8], np.float32))[0] == 0x3F80  # tie to even
+    assert oracle.f32_to_bf16(np.array([1 + 3 * 2 ** -8], np.float32))[0] == 0x3F82
+    assert np.isnan(oracle.bf16_to_f32(oracle.f32_to_bf16(np.array([np.nan], np.float32))))[0]
+
+
+def test_expf_accuracy_and_special_cases():
+    x = np.linspace(-80, 88, 2_000_001, dtype=np.float32)
+    got = oracle.expf(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    rel = np.abs(got - ref) / ref
+    assert rel.max() < 2.5 * 2 ** -23, rel.max()  # within ~2 ulp of float32
+    assert oracle.expf(np.array([0.0], np.float32))[0] == 1.0
+    sp = oracle.expf(np.array([-81.0, -np.inf, np.inf, 89.0, np.nan], np.float32))
+    assert sp[0] == 0 and sp[1] == 0 and np.isinf(sp[2]) and np.isinf(sp[3]) and np.isnan(sp[4])
+    # monotone on a fine grid
+    g = oracle.expf(np.linspace(-5, 5, 100001, dtype=np.float32))
+    assert np.all(np.diff(g) >= 0)
+
+
+# ---------------------------------------------------------------- affine format
+
+def np_dequant(q, s, b, group=64, msb_first=False):
+    """native_affine_ops.py:29-36 restated: LSB-first nibbles, codes*S + B."""
+    shifts = np.arange(8, dtype=np.uint32) * 4
+    if msb_first:
+        shifts = shifts[::-1]
+    codes = (q.astype(np.uint32)[..., None] >> shifts) & 0xF
+    codes = codes.reshape(*q.shape[:-1], q.shape[-1] * 8).astype(np.float64)
+    return codes * np.repeat(f(s), group, -1) + np.repeat(f(b), group, -1)
+
+
+def rand_affine(E, N, Kin):
+    q = RNG.integers(0, 2 ** 32, size=(E, N, Kin // 8), dtype=np.uint64).astype(np.uint32)
+    s = bf(RNG.uniform(0.005, 0.02, size=(E, N, Kin // 64)))
+    b = bf(-8 * f(s))
+    return q, s, b
+
+
+def test_dequant_closed_form_and_nibble_order():
+    q, s, b = rand_affine(1, 16, 256)
+    got = oracle.dequant_f64(q[0], s[0], b[0])
+    np.testing.assert_array_equal(got, np_dequant(q[0], s[0], b[0]))
+    # a single word 0x76543210 decodes to codes 0..7 in element order
+    qq = np.full((1, 8), 0x76543210, np.uint32)
+    one = bf(np.ones((1, 1)))
+    zero = bf(np.zeros((1, 1)))
+    np.testing.assert_array_equal(oracle.dequant_f64(qq, one, zero)[0, :8], np.arange(8))
+    # planted mistake: MSB-first nibble order is detected
+    assert not np.array_equal(got, np_dequant(q[0], s[0], b[0], msb_first=True))
+    # bias = -8 scale makes dequant exact: s * (q - 8)
+    codes = np_dequant(q[0], bf(np.ones_like(f(s[0]))), bf(np.zeros_like(f(s[0]))))
+    np.testing.assert_array_equal(got, (codes - 8) * np.repeat(f(s[0]), 64, -1))
+
+
+def test_gather_qmm_brute_force_tiny():
+    E, N, Kin, rows = 3, 8, 128, 11
+    q, s, b = rand_affine(E, N, Kin)
+    x = bf(RNG.standard_normal((5, Kin)))
+    xrow = RNG.integers(0, 5, rows).astype(np.int32)
+    eid = RNG.integers(0, E, rows).astype(np.int32)
+    got = oracle.gather_qmm_f64(x, xrow, eid, q, s, b)
+    w = np_dequant(q, s, b)
+    for r in range(rows):
+        ref = w[eid[r]] @ f(x[xrow[r]])
+        np.testing.assert_allclose(got[r], ref, rtol=1e-12, atol=1e-12)
+    # planted mistake: the transposed operand (x . W instead of x . W^T) does not fit
+    assert not np.allclose(got[0], (f(x[xrow[0]])[:N] * 0 + w[eid[0]][:, :N].T @ f(x[xrow[0]])[:N]))
+
+
+# ---------------------------------------------------------------- router
+
+def test_router_logits_one_hot_exact_and_tolerance():
+    E, H = 40, 1536
+    w = bf(RNG.standard_normal((E, H)) * 0.02)
+    bias = RNG.standard_normal(E).astype(np.float32)
+    x = np.zeros((H, H), np.float32)
+    sel = RNG.choice(H, 7, replace=False)
+    x = bf(np.eye(H, dtype=np.float32)[sel])  # rows e_h
+    got = oracle.router_logits(x, w)
+    np.testing.assert_array_equal(got, w[:, sel].T)  # exactly w[e, h]
+    got_b = oracle.router_logits(x, w, bias)
+    np.testing.assert_array_equal(got_b, bf(f(w[:, sel].T) + bias))
+    # general rows: within one bf16 rounding of the float64 product
+    xr = bf(RNG.standard_normal((16, H)))
+    ref = f(xr) @ f(w).T
+    gotr = f(oracle.router_logits(xr, w))
+    assert np.max(np.abs(gotr - ref) / np.maximum(np.abs(ref), 1e-3)) < 2 ** -7
+    # planted mistake: a dropped bias is detected
+    assert not np.array_equal(oracle.router_logits(xr, w, bias), oracle.router_logits(xr, w))
+
+
+def test_olmoe_softmax_close_to_float64():
+    lg = bf(RNG.standard_normal((500, 64)) * 2)
+    p = f(oracle.olmoe_softmax(lg))
+    x = f(lg)
+    ref = np.exp(x - x.max(1, keepdims=True))
+    ref /= ref.sum(1, keepdims=True)
+    assert np.max(np.abs(p - ref) / ref) <= 2 ** -8  # one bf16 rounding
+    assert np.allclose(p.sum(1), 1, atol=0.02)
+
+
+def stable_topk_desc_nan_last(v, k):
+    """The reference torch body of native_olmoe_topk_indices
+    (argsort(-x, stable)[..., :k], native_affine_ops.py:146) with NaN last."""
+    out = []
+    for r in v:
+        nan = np.isnan(r)
+        out.append(np.lexsort((np.where(nan, 0, -r), nan))[:k])
+    return np.array(out, np.int32)
+
+
+def tie_logits(T, E):
+    v = RNG.integers(-6, 6, size=(T, E)).astype(np.float32) * 0.25
+    v[0] = 0.5
+    v[1, 3 % E] = np.nan
+    v[2, ::7] = np.nan
+    v[3] = np.nan
+    v[4, 5 % E] = np.inf
+    v[5, 9 % E] = -np.inf
+    return bf(v)
+
+
+@pytest.mark.parametrize("E,K", [(64, 8), (40, 8), (7, 3), (1, 1)])
+def test_olmoe_route_rule(E, K):
+    for lg in (tie_logits(64, E), bf(RNG.standard_normal((300, E)))):
+        idx, gates = oracle.route_olmoe(lg, K)
+        p = oracle.olmoe_softmax(lg)
+        np.testing.assert_array_equal(idx, stable_topk_desc_nan_last(f(p), K))
+        np.testing.assert_array_equal(gates, np.take_along_axis(p, idx.astype(np.int64), 1))
+        # K distinct experts per token
+        assert all(len(set(r)) == K for r in idx)
+    # planted mistake: ties resolved to the higher id do not match the rule
+    lg = bf(np.full((1, E), 0.5, np.float32))
+    idx, _ = oracle.route_olmoe(lg, K)
+    np.testing.assert_array_equal(idx[0], np.arange(K))
+    assert E == K or not np.array_equal(idx[0], np.arange(E)[::-1][:K])
+
+
+@pytest.mark.parametrize("E,K", [(40, 8), (64, 8), (7, 3), (64, 64)])
+def test_granite_route_rule(E, K):
+    for lg in (tie_logits(64, E), bf(RNG.standard_normal((300, E)))):
+        idx, gates = oracle.route_granite(lg, K)
+        v = f(lg)
+        # native_topk_indices lowering: argpartition(kth=-k) + slice of the last k, with a
+        # stable ascending order (NaN last): the last k of the stable ascending sort.
+        order = np.array([np.lexsort((np.where(np.isnan(r), 0, r), np.isnan(r))) for r in v])
+        np.testing.assert_array_equal(idx, order[:, E - K:])
+        sel = np.take_along_axis(v, idx.astype(np.int64), 1)
+        fin = np.all(np.isfinite(sel), 1)
+        ref = np.exp(sel[fin] - sel[fin].max(1, keepdims=True))
+        ref /= ref.sum(1, keepdims=True)
+        np.testing.assert_allclose(gates[fin], ref, rtol=3e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------- grouping
+
+@pytest.mark.parametrize("n,E", [(0, 4), (1, 1), (64, 64), (1000, 40), (32768, 64)])
+def test_group_is_stable_counting_sort(n, E):
+    ids = RNG.integers(0, E, n).astype(np.int32)
+    order, inverse, offsets = oracle.group(ids, E)
+    np.testing.assert_array_equal(order, np.argsort(ids, kind="stable"))
+    np.testing.assert_array_equal(inverse[order], np.arange(n))
+    np.testing.assert_array_equal(offsets, np.concatenate([[0], np.cumsum(np.bincount(ids, minlength=E))]))
+    if n:
+        assert np.all(np.diff(ids[order]) >= 0)
+
+
+def test_group_rejects_bad_ids():
+    with pytest.raises(ValueError):
+        oracle.group(np.array([0, 5, 2], np.int32), 4)
+
+
+# ---------------------------------------------------------------- the block
+
+class W:
+    pass
+
+
+def tiny_block(E=4, H=128, I=64):
+    w = W()
+    for proj, (N, Kin) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+        q, s, b = rand_affine(E, N, Kin)
+        setattr(w, proj + "_q", q)
+        setattr(w, proj + "_s", s)
+        setattr(w, proj + "_b", b)
+    return w
+
+
+def np_block(x, idx, gates, w, residual=None, rm=1.0, swap_gate_up=False):
+    """Independent float64 MoE block: dequant -> gate/up -> SwiGLU -> down -> combine."""
+    G = np_dequant(w.gate_q, w.gate_s, w.gate_b)
+    U = np_dequant(w.up_q, w.up_s, w.up_b)
+    D = np_dequant(w.down_q, w.down_s, w.down_b)
+    if swap_gate_up:
+        G, U = U, G
+    xs = f(x)
+    y = np.zeros_like(xs)
+    for t in range(xs.shape[0]):
+        for k in range(idx.shape[1]):
+            e = idx[t, k]
+            g = G[e] @ xs[t]
+            u = U[e] @ xs[t]
+            h = g / (1 + np.exp(-g)) * u
+            y[t] += gates[t, k] * (D[e] @ h)
+    y *= rm
+    if residual is not None:
+        y += f(residual)
+    return y
+
+
+def test_moe_reference_matches_independent_block():
+    w = tiny_block()
+    x = bf(RNG.standard_normal((6, 128)))
+    idx = RNG.integers(0, 4, (6, 2)).astype(np.int32)
+    gates = RNG.random((6, 2)).astype(np.float32)
+    res = bf(RNG.standard_normal((6, 128)))
+    got = oracle.moe_reference(x, idx, gates, w, residual=res, rm=0.5)
+    ref = np_block(x, idx, gates, w, residual=res, rm=0.5)
+    np.testing.assert_allclose(got, ref, rtol=1e-10, atol=1e-10)
+    # planted mistakes fail the same comparison
+    assert not np.allclose(got, np_block(x, idx, gates, w, residual=res, rm=0.5, swap_gate_up=True))
+    assert not np.allclose(got, np_block(x, idx, gates, w, residual=res, rm=1.0))
+    sub = oracle.moe_reference(x, idx, gates, w, tokens=np.array([4, 1], np.int32), residual=res, rm=0.5)
+    np.testing.assert_allclose(sub, ref[[4, 1]], rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("route", ["olmoe", "granite"])
+def test_cpu_block_matches_reference(route):
+    E, H, I, K = 8, 256, 128, 2
+    w = tiny_block(E, H, I)
+    router = bf(RNG.standard_normal((E, H)) * 0.02)
+    x = bf(RNG.standard_normal((40, H)))
+    y, idx, gates, used = oracle.moe_block_cpu(x, w, route, router, top_k=K, threads=2)
+    lg = oracle.router_logits(x, router)
+    if route == "olmoe":
+        ridx, rg = oracle.route_olmoe(lg, K)
+        rg = f(rg)
+    else:
+        ridx, rg = oracle.route_granite(lg, K)
+    np.testing.assert_array_equal(idx, ridx)
+    ref = oracle.moe_reference(x, ridx, rg.astype(np.float32), w)
+    err = np.abs(f(y) - ref).max() / np.abs(ref).max()
+    assert err < 1e-2, err
+    assert used >= 1

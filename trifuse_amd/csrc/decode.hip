@@ -196,6 +196,47 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(const uint16_t* __re
   }
 }
 
+// Any H % 64 == 0: the same arithmetic as decode_route_kernel with scalar loads.
+template <int ROUTE>
+__global__ __launch_bounds__(1024) void decode_route_generic(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             int H, int E, int K,
+                                                             uint16_t* __restrict__ logits,
+                                                             int32_t* __restrict__ idx,
+                                                             float* __restrict__ gates) {
+  __shared__ uint16_t s_logit[64];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = H / 64;
+  for (int e = wave; e < E; e += 16) {
+    float s = 0.0f;
+    for (int j = 0; j < c; ++j)
+      s = __builtin_fmaf(bf2f(x[(int64_t)t * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
+    s = group_sum<64>(s);
+    if (lane == 0) {
+      const uint16_t lb = f2bf(bias ? s + bias[e] : s);
+      s_logit[e] = lb;
+      if (logits) logits[(int64_t)t * E + e] = lb;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float g;
+  int id;
+  if (ROUTE == TFM_ROUTE_OLMOE) {
+    uint16_t gb;
+    id = olmoe_route_wave(s_logit, E, K, &g, &gb);
+  } else {
+    id = granite_route_wave(s_logit, E, K, &g);
+  }
+  if (lane < K) {
+    idx[(int64_t)t * K + lane] = id;
+    gates[(int64_t)t * K + lane] = g;
+  }
+}
+
 static int lg_for(int kin) {
   const int nch = kin / 32;
   return nch <= 4 ? 4 : nch <= 8 ? 8 : nch <= 16 ? 16 : nch <= 32 ? 32 : 64;
@@ -222,7 +263,13 @@ void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* rout
     case 2048: TFM_DR(32) break;
     case 3072: TFM_DR(48) break;
     case 4096: TFM_DR(64) break;
-    default: fail(TFM_E_UNSUPPORTED, "decode routing: hidden width not built");
+    default:
+      if (route_kind == TFM_ROUTE_OLMOE)
+        decode_route_generic<TFM_ROUTE_OLMOE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K, logits,
+                                                                 idx, gates);
+      else
+        decode_route_generic<TFM_ROUTE_GRANITE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K,
+                                                                   logits, idx, gates);
   }
 #undef TFM_DR
   check_hip(hipGetLastError(), "decode route launch");

@@ -180,10 +180,18 @@ def make_x(geom: Geometry, tokens: int, tag: str = "x") -> torch.Tensor:
     return normal_bf16((tokens, geom.hidden), 1.0, _key(geom.name, tag, tokens))
 
 
-def workload_layers(wl: Workload, device="cpu") -> List[LayerWeights]:
-    # The two Granite workloads share one layer's weights (prefill then decode).
+def workload_layers(wl: Workload, device="cpu", layers: Optional[int] = None) -> List[LayerWeights]:
+    """Independently seeded layers of a workload (default: the workload's own
+    layer count). The two Granite workloads share weights (prefill then decode)."""
     tag = "shared" if wl.geometry is GRANITE else wl.name
-    return [make_layer(wl.geometry, l, device, zipf=wl.zipf, seed_tag=tag) for l in range(wl.layers)]
+    n = wl.layers if layers is None else layers
+    return [make_layer(wl.geometry, l, device, zipf=wl.zipf, seed_tag=tag) for l in range(n)]
+
+
+# Distinct layers a timing loop rotates through: 16 layers of either geometry
+# exceed MI355X's 256 MB last-level cache several times over, so every step
+# reads its expert weights from HBM, as a model's layer stack would.
+TIMING_LAYERS = 16
 
 
 def workload_x(wl: Workload) -> torch.Tensor:
@@ -210,5 +218,5 @@ def gemm_flops(geom: Geometry, routes: int, which: str) -> int:
 __all__ = [
     "Geometry", "Workload", "OLMOE", "GRANITE", "WORKLOADS", "LayerWeights", "make_layer",
     "make_x", "workload_layers", "workload_x", "algorithmic_bytes", "algorithmic_flops",
-    "gemm_flops", "hash_u32", "SEED", "GROUP",
+    "gemm_flops", "hash_u32", "SEED", "GROUP", "TIMING_LAYERS",
 ]
