@@ -54,7 +54,7 @@ extern "C" {
 #define TFM_ROUTER_AFFINE 1 /* affine-quantised router (not built yet)     */
 
 /* tfm_moe_forward / tfm_moe_experts flags */
-#define TFM_FLAG_DETERMINISTIC 1u /* ordered K reduction (no atomics) at any T */
+#define TFM_FLAG_DETERMINISTIC 1u /* accepted for compatibility: every path reduces the K routes of a token in k order */
 
 /* Bits of the device status word (tfm_status_word). */
 #define TFM_STATUS_BAD_EXPERT_ID 1u /* an expert id outside [0, E) was seen   */

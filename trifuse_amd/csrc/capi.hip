@@ -6,6 +6,7 @@
 // residual. The grouping is always the stable expert sort (the reference sorts
 // once T*K >= 64; with fewer routes it gathers per route, which yields the
 // same per-route results).
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -117,6 +118,7 @@ struct BlockWs {
   Grouping grp;
   uint16_t* h;
   float* P;  // [R, H] sorted rows; the atomic path uses its start as acc [T, H]
+  int32_t* hist;  // grouping chunk histograms
   size_t bytes;
 };
 
@@ -135,6 +137,9 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.grp.E = g.num_experts;
   w.h = c.take<uint16_t>((size_t)(R * g.intermediate_size));
   w.P = c.take<float>((size_t)(R * g.hidden_size));
+  const int64_t chunks = std::max<int64_t>(group_blocks(R, kGroupChunk),
+                                           group_blocks(R, kTopkTokensPerBlock * g.experts_per_token));
+  w.hist = c.take<int32_t>((size_t)((chunks + 1) * (g.num_experts + 1)));
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -149,6 +154,7 @@ static bool fused_decode(const tfm_geometry& g, int64_t R) {
 struct GroupWs {
   WsHeader* hdr;
   Grouping grp;
+  int32_t* hist;
   size_t bytes;
 };
 
@@ -161,6 +167,7 @@ static GroupWs carve_group(int64_t n, int E, void* base) {
   w.grp.offsets = c.take<int32_t>((size_t)E + 1);
   w.grp.active = c.take<int32_t>((size_t)E + 1);
   w.grp.E = E;
+  w.hist = c.take<int32_t>((size_t)((group_blocks(n, kGroupChunk) + 1) * (E + 1)));
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -203,16 +210,18 @@ static int gemv_threshold() {
 }
 
 // Expert part of the block on grouped routes (flat routes t*K+k of idx).
+// `grouped`: the routes in ws.grp already come grouped (prefill forward path).
 static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const uint16_t* residual,
                         const int32_t* idx, const float* gates, const tfm_moe_weights* w,
-                        uint16_t* y, uint32_t flags, BlockWs& ws, hipStream_t s) {
+                        uint16_t* y, uint32_t flags, BlockWs& ws, hipStream_t s,
+                        bool grouped = false) {
   const tfm_geometry& g = p->g;
   const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
   const int64_t R = T * K;
   const bool gemv = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
-  {
+  if (!grouped) {
     StageScope st(TFM_STAGE_GROUP, s);
-    launch_group(idx, R, E, ws.grp, &ws.hdr->status, s);
+    launch_group(idx, R, E, ws.grp, ws.hist, &ws.hdr->status, s);
   }
   const int max_active = (int)(R < E ? R : E);
   const RowMap rm{ws.grp.order, nullptr, K, T, &ws.hdr->status};
@@ -228,30 +237,22 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     StageScope st(TFM_STAGE_COMBINE, s);
     launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
                           g.residual_multiplier, y, s);
-  } else if (flags & TFM_FLAG_DETERMINISTIC) {
-    {
-      StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, nullptr, 0, s);
-    }
-    {
-      StageScope st(TFM_STAGE_DOWN, s);
-      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, gates, K, nullptr, ws.P, s);
-    }
-    StageScope st(TFM_STAGE_COMBINE, s);
-    launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
-                          g.residual_multiplier, y, s);
   } else {
-    float* acc = ws.P;
+    // Prefill: the down projection writes bf16 expert outputs in sorted
+    // order (into the P region), the combine weights and sums them per token.
+    (void)flags;
+    uint16_t* Y = reinterpret_cast<uint16_t*>(ws.P);
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, acc, T * H, s);
+      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, s);
     }
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, gates, K, acc, nullptr, s);
+      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, Y, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
-    launch_finalize_acc(acc, (int)T, H, residual, g.residual_multiplier, y, s);
+    launch_combine_rows(Y, ws.grp.inverse, ws.grp.offsets + E, gates, (int)T, K, H, residual,
+                        g.residual_multiplier, y, s);
   }
 }
 
@@ -391,7 +392,7 @@ int tfm_group(const int32_t* expert_ids, int64_t n_routes, int32_t num_experts, 
     gout.order = order;
     gout.inverse = inverse;
     gout.offsets = offsets;
-    launch_group(expert_ids, n_routes, num_experts, gout, &ws.hdr->status,
+    launch_group(expert_ids, n_routes, num_experts, gout, ws.hist, &ws.hdr->status,
                  static_cast<hipStream_t>(stream));
   });
 }
@@ -433,7 +434,7 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     need_align16(x, "x");
     check_affine(*w, "w");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    launch_group(rhs_indices, rows, num_experts, ws.grp, &ws.hdr->status, s);
+    launch_group(rhs_indices, rows, num_experts, ws.grp, ws.hist, &ws.hdr->status, s);
     // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
     const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
     const int max_active = (int)(rows < num_experts ? rows : num_experts);
@@ -525,14 +526,17 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
     }
     {
       StageScope st(TFM_STAGE_TOPK, s);
-      launch_topk(g.route, ws.logits, (int)tokens, g.num_experts, g.experts_per_token, ws.idx,
-                  nullptr, ws.gates, s);
+      launch_topk_hist(g.route, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
+    }
+    {
+      StageScope st(TFM_STAGE_GROUP, s);
+      launch_group_scatter(ws.idx, R, E, kTopkTokensPerBlock * K, ws.hist, ws.grp, &ws.hdr->status, s);
     }
     if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
     if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
                                    reinterpret_cast<int32_t*>(gates_out), R, s);
     run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
-                ws.idx, ws.gates, weights, static_cast<uint16_t*>(y), flags, ws, s);
+                ws.idx, ws.gates, weights, static_cast<uint16_t*>(y), flags, ws, s, true);
   });
 }
 
@@ -546,6 +550,7 @@ size_t tfm_expert_routes_workspace_bytes(const tfm_plan* plan, int64_t n_routes)
   c.take<int32_t>((size_t)g.num_experts + 1);  // active
   c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
   c.take<float>((size_t)(n_routes * g.hidden_size));
+  c.take<int32_t>((size_t)((group_blocks(n_routes, kGroupChunk) + 1) * (g.num_experts + 1)));
   return align_up(c.offset, 256);
 }
 
@@ -579,20 +584,21 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     grp.E = g.num_experts;
     uint16_t* h = c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
     float* P = c.take<float>((size_t)(n_routes * g.hidden_size));
+    int32_t* hist = c.take<int32_t>((size_t)((group_blocks(n_routes, kGroupChunk) + 1) * (g.num_experts + 1)));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts;
-    launch_group(expert_ids, n_routes, E, grp, &hdr->status, s);
+    launch_group(expert_ids, n_routes, E, grp, hist, &hdr->status, s);
     const RowMap rm{grp.order, token_indices, 1, tokens, &hdr->status};
     const int max_active = (int)(n_routes < E ? n_routes : E);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048) {
       launch_gemv_gateup(xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
       launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
+      launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
     } else {
-      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, h, nullptr, 0, s);
-      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, nullptr, 1, nullptr, P, s);
+      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, h, s);
+      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, static_cast<uint16_t*>(out_sorted), s);
     }
-    launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
   });
 }
 

@@ -2,9 +2,11 @@
 //
 // The reference combines the K expert outputs of a token with the routing
 // gates and adds the residual (MLXNativeGraniteMoEPrefill.h:688-701, kernel
-// text :54-70). Here the down projection already multiplied each route's
-// output by its gate; the K rows are summed in k order in fp32, scaled by the
-// residual multiplier, added to the residual and rounded once to bf16.
+// text :54-70). Both combines sum the K routes of a token in k order in fp32,
+// scale by the residual multiplier, add the residual and round once to bf16:
+// combine_sorted takes rows the decode down projection already multiplied by
+// their gates (fp32), combine_rows takes the prefill path's bf16 expert
+// outputs and applies the gates itself.
 #include "tfm_device.h"
 #include "tfm_internal.h"
 
@@ -60,35 +62,64 @@ void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t
   check_hip(hipGetLastError(), "combine launch");
 }
 
-__global__ __launch_bounds__(256) void finalize_acc_kernel(const float* __restrict__ acc, int T,
-                                                           int H, const uint16_t* __restrict__ residual,
+// 8 columns per thread; H % 8 == 0. Y rows are bf16 expert outputs (the
+// reference's per-route gather_qmm output, MLXNativeGraniteMoEPrefill.h:684),
+// weighted by the fp32 gate and summed in k order.
+__global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __restrict__ Y,
+                                                           const int32_t* __restrict__ inverse,
+                                                           const int32_t* __restrict__ n_valid,
+                                                           const float* __restrict__ gates,
+                                                           int T, int K, int H,
+                                                           const uint16_t* __restrict__ residual,
                                                            float rmul, uint16_t* __restrict__ y) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)T * H / 8) return;
-  const int64_t base = i * 8;
-  const float4* p = reinterpret_cast<const float4*>(acc + base);
-  const float4 a = p[0], b = p[1];
-  const float s[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int per_row = H / 8;
+  if (i >= (int64_t)T * per_row) return;
+  const int t = (int)(i / per_row), c = (int)(i % per_row) * 8;
+  float s[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) s[v] = 0.0f;
+  const int nv = *n_valid;
+  for (int k = 0; k < K; ++k) {
+    const int64_t f = (int64_t)t * K + k;
+    const int64_t row = inverse[f];
+    if (row >= nv) continue;
+    const float gw = gates[f];
+    const uint4 a = *reinterpret_cast<const uint4*>(Y + row * H + c);
+    s[0] = __builtin_fmaf(gw, lo_bf(a.x), s[0]);
+    s[1] = __builtin_fmaf(gw, hi_bf(a.x), s[1]);
+    s[2] = __builtin_fmaf(gw, lo_bf(a.y), s[2]);
+    s[3] = __builtin_fmaf(gw, hi_bf(a.y), s[3]);
+    s[4] = __builtin_fmaf(gw, lo_bf(a.z), s[4]);
+    s[5] = __builtin_fmaf(gw, hi_bf(a.z), s[5]);
+    s[6] = __builtin_fmaf(gw, lo_bf(a.w), s[6]);
+    s[7] = __builtin_fmaf(gw, hi_bf(a.w), s[7]);
+  }
+  float r[8];
   if (residual) {
-    const uint4 rv = *reinterpret_cast<const uint4*>(residual + base);
+    const uint4 rv = *reinterpret_cast<const uint4*>(residual + (int64_t)t * H + c);
     r[0] = lo_bf(rv.x); r[1] = hi_bf(rv.x); r[2] = lo_bf(rv.y); r[3] = hi_bf(rv.y);
     r[4] = lo_bf(rv.z); r[5] = hi_bf(rv.z); r[6] = lo_bf(rv.w); r[7] = hi_bf(rv.w);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) r[v] = 0.0f;
   }
   uint4 o;
   o.x = pack_bf16x2(r[0] + rmul * s[0], r[1] + rmul * s[1]);
   o.y = pack_bf16x2(r[2] + rmul * s[2], r[3] + rmul * s[3]);
   o.z = pack_bf16x2(r[4] + rmul * s[4], r[5] + rmul * s[5]);
   o.w = pack_bf16x2(r[6] + rmul * s[6], r[7] + rmul * s[7]);
-  *reinterpret_cast<uint4*>(y + base) = o;
+  *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
 }
 
-void launch_finalize_acc(const float* acc, int T, int H, const uint16_t* residual, float rmul,
-                         uint16_t* y, hipStream_t s) {
+void launch_combine_rows(const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
+                         const float* gates, int T, int K, int H, const uint16_t* residual,
+                         float rmul, uint16_t* y, hipStream_t s) {
   if (T <= 0) return;
-  const int64_t n = (int64_t)T * H / 8;
-  finalize_acc_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(acc, T, H, residual, rmul, y);
-  check_hip(hipGetLastError(), "finalize launch");
+  const int64_t n = (int64_t)T * (H / 8);
+  combine_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(Y, inverse, n_valid, gates, T, K,
+                                                                 H, residual, rmul, y);
+  check_hip(hipGetLastError(), "combine launch");
 }
 
 __global__ void rows_to_bf16_kernel(const float* __restrict__ P, int64_t n, uint16_t* __restrict__ out) {
@@ -101,17 +132,6 @@ void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hip
   if (n <= 0) return;
   rows_to_bf16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, n, out);
   check_hip(hipGetLastError(), "rows_to_bf16 launch");
-}
-
-__global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
-
-void launch_fill_f32(float* p, int64_t n, float v, hipStream_t s) {
-  if (n <= 0) return;
-  fill_f32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n, v);
-  check_hip(hipGetLastError(), "fill launch");
 }
 
 __global__ void copy_i32_kernel(const int32_t* __restrict__ a, int32_t* __restrict__ b, int64_t n) {

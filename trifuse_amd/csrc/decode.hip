@@ -173,8 +173,8 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(const uint16_t* __re
       s = __builtin_fmaf(xv[8 * i + 6], lo_bf(v.w), s);
       s = __builtin_fmaf(xv[8 * i + 7], hi_bf(v.w), s);
     }
-    s = group_sum<64>(s);
-    if (lane == 0) {
+    s = wave_tree_sum64(s);
+    if (lane == 63) {
       const uint16_t lb = f2bf(bias ? s + bias[e] : s);
       s_logit[e] = lb;
       if (logits) logits[(int64_t)t * E + e] = lb;
@@ -214,8 +214,8 @@ __global__ __launch_bounds__(1024) void decode_route_generic(const uint16_t* __r
     float s = 0.0f;
     for (int j = 0; j < c; ++j)
       s = __builtin_fmaf(bf2f(x[(int64_t)t * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
-    s = group_sum<64>(s);
-    if (lane == 0) {
+    s = wave_tree_sum64(s);
+    if (lane == 63) {
       const uint16_t lb = f2bf(bias ? s + bias[e] : s);
       s_logit[e] = lb;
       if (logits) logits[(int64_t)t * E + e] = lb;

@@ -1,73 +1,150 @@
 // Prefill path: grouped GEMM over expert-contiguous routes.
 //
-// Each workgroup computes a BM x BN tile of one expert's output. Per K step of
-// 64 (one quantisation group) it
-//   * gathers BM activation rows (x rows of the routed tokens, or rows of the
-//     expert-sorted SwiGLU output) into LDS as bf16,
-//   * loads the packed 4-bit weight rows, dequantises them in registers
+// Each workgroup computes a BM x BN tile of one expert's output with eight
+// waves, two per SIMD, so that one wave's loads, dequantisation and LDS
+// traffic overlap the other's MFMAs. Per K step of 64 (one quantisation
+// group) it
+//   * copies BM activation rows (x rows of the routed tokens, or rows of the
+//     expert-sorted SwiGLU output) from global memory straight into LDS
+//     (buffer loads with an LDS destination),
+//   * loads BN packed 4-bit weight rows into registers, dequantises them
 //     (s*q+b in fp32, rounded to bf16) and writes them to LDS,
-//   * runs v_mfma_f32_32x32x16_bf16 on the two LDS tiles,
-// double-buffered so the next step's global loads are in flight during the
-// MFMAs. LDS rows are 64 bf16 (8 chunks of 16 B); chunk c of row r is stored
-// at c ^ (r & 7), which makes the MFMA fragment reads conflict-free.
-// Epilogues: SwiGLU (gate/up), gate-weighted scatter-add into an fp32
-// accumulator or gate-weighted store into sorted rows (down), plain bf16
-// scatter (gather_qmm).
+//   * runs v_mfma_f32_32x32x16_bf16 on the two LDS tiles, each wave owning a
+//     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane).
+//
+// Pipeline: two LDS stages for each operand. While the MFMAs of step k read
+// stage k%2, the activations of step k+1 are copied into stage (k+1)%2, the
+// packed weights of step k+1 (loaded during step k-1) are dequantised into
+// stage (k+1)%2 and the packed weights of step k+2 are loaded; one barrier
+// per step.
+//
+// LDS rows are 64 bf16 (8 chunks of 16 B); chunk c of row r is stored at
+// c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128 pass (16 consecutive
+// rows, one chunk) hit 16 distinct 16-byte bank groups.
+//
+// Rows outside the segment and weight rows past N get a buffer offset beyond
+// the buffer and read as zero, so the loop has no divergent branches.
+//
+// Epilogue: each wave converts its accumulators (SwiGLU for gate/up) to bf16
+// in a private LDS block, 32 rows at a time, and writes them out as 16-byte
+// row chunks: h rows (gate/up), expert-output rows in sorted order (down) or
+// rows scattered to their flat route (gather_qmm).
+#include <cstdlib>
+#include <type_traits>
+
 #include "tfm_device.h"
 #include "tfm_internal.h"
 
 namespace tfm {
 
-constexpr int BM = 128;
-constexpr int BN = 128;  // weight rows per tile (gate/up: 64 gate + 64 up)
 constexpr int BK = 64;
-constexpr int kThreads = 256;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset that reads as zero
 
 enum GgemmMode { kGgGateUp = 0, kGgDown = 1, kGgPlain = 2 };
 
 struct GgArgs {
   const uint16_t* x;     // activations (x rows, or sorted h rows for down)
+  uint32_t x_bytes;      // size of x (buffer range)
   RowMap rm;
   Grouping g;
   tfm_affine wa, wb;     // gate/up (wb unused otherwise)
   int N;                 // output columns of one matrix
   int Kin;
-  const float* gates;    // down: fp32 gate per flat route (null: 1)
-  int K;                 // routes per token (down, atomic mode)
-  float* acc;            // down: fp32 [T, N] accumulator (atomic mode)
-  float* P;              // down: fp32 [n_routes, N] (deterministic mode)
-  uint16_t* out;         // gate/up: h [n_routes, N]; plain: out [rows, N]
-  float* zero_buf;       // optional region zeroed by this launch
-  int64_t zero_count;
+  uint16_t* out;         // gate/up: h [n_routes, N]; down: y [n_routes, N]; plain: out [rows, N]
 };
 
-// Row/column of accumulator element v of lane `lane` inside a 32x32 block of
-// v_mfma_f32_32x32x16_bf16 (operands: lane l supplies row/column l%32 and
-// k = 8*(l/32) .. 8*(l/32)+7).
+// Row of accumulator element v of lane `lane` inside a 32x32 block of
+// v_mfma_f32_32x32x16_bf16 (its column is lane % 32; operands: lane l
+// supplies row/column l%32 and k = 8*(l/32) .. 8*(l/32)+7).
 __device__ __forceinline__ int acc_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
-__device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void ggemm_kernel(GgArgs args) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * BK];
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gg_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 8 nibbles (one 32-bit word of a weight row) -> 8 bf16 (s*q+b).
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
+  float d[8];
+  dequant8(w, s, b, d);
+  uint4 pk;
+  pk.x = pack_bf16x2(d[0], d[1]);
+  pk.y = pack_bf16x2(d[2], d[3]);
+  pk.z = pack_bf16x2(d[4], d[5]);
+  pk.w = pack_bf16x2(d[6], d[7]);
+  return pk;
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int k) {
+  return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+}
+
+// silu(g) * u with the hardware exp and reciprocal (relative error ~1e-7,
+// far below the bf16 rounding that follows).
+__device__ __forceinline__ float swiglu(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+// 16 bytes per lane from a buffer into LDS: lane l writes dst + 16*l (dst is
+// wave-uniform). Out-of-range offsets deliver zeros.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+#else
+  (void)r; (void)dst; (void)voff; (void)soff;
+#endif
+}
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE>
+struct GgCfg {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int WAVES = WAVES_M * WAVES_N;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int MB = WM / 32;                // 32-row MFMA blocks per wave
+  static constexpr int NB = WN / 32;                // 32-column MFMA blocks per wave
+  static constexpr int LA = BM / (8 * WAVES);       // 8-row LDS copies per wave per step
+  static constexpr int LB = BN * 2 / THREADS;       // packed 16-byte chunks per thread per step
+  static constexpr int OUT_COLS = MODE == kGgGateUp ? BN / 2 : BN;
+  static constexpr int WCOLS = MODE == kGgGateUp ? WN / 2 : WN;   // output columns per wave
+  static constexpr int SROW = WCOLS + 8;            // staging row stride (bf16), 16 B pad
+  static_assert(LA >= 1 && LA * 8 * WAVES == BM, "A copies must tile the block rows");
+  static_assert(LB >= 1 && LB * THREADS == BN * 2, "B chunks must tile the block columns");
+  static_assert(LB * 4 >= 3, "B words are spread over three sub-steps");
+  static_assert(MODE != kGgGateUp || NB % 2 == 0, "gate/up wave tiles pair gate and up blocks");
+  static_assert(WAVES % 4 == 0, "staging blocks are spread over the four LDS stages");
+  static_assert(32 * SROW * (WAVES / 4) <= BM * BK, "epilogue staging must fit in an A stage");
+};
+
+// Packed weights of one K step for one thread.
+template <int LB>
+struct RawB {
+  uint4 b[LB];
+  uint32_t s[LB], bias[LB];
+};
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE>
+__global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgArgs args) {
+  using C = GgCfg<BM_, BN_, WAVES_M_, WAVES_N_, MODE>;
+  constexpr int BM = C::BM, BN = C::BN, MB = C::MB, NB = C::NB, LA = C::LA, LB = C::LB;
+  constexpr int T = C::THREADS;
+  // Two stages each of A and B, as separate objects so that the compiler's
+  // wait tracking tells LDS copies into one stage from reads of the other.
+  __shared__ __attribute__((aligned(16))) uint16_t sA0[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t sA1[BM * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t sB0[BN * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t sB1[BN * BK];
   __shared__ int s_tiles[65];
   __shared__ int s_expert;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int E = args.g.E;
-
-  if (args.zero_buf) {
-    const int64_t n4 = args.zero_count / 4;
-    float4* z = reinterpret_cast<float4*>(args.zero_buf);
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + tid; i < n4; i += (int64_t)gridDim.x * kThreads)
-      z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (blockIdx.x == 0)
-      for (int64_t i = n4 * 4 + tid; i < args.zero_count; i += kThreads) args.zero_buf[i] = 0.f;
-  }
 
   // M-tile prefix over experts.
   if (tid < 64) {
@@ -76,7 +153,6 @@ __global__ __launch_bounds__(kThreads, 2) void ggemm_kernel(GgArgs args) {
       const int cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
       t = (cnt + BM - 1) / BM;
     }
-    // inclusive scan across the wave
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int o = __shfl_up(t, d, 64);
@@ -86,7 +162,7 @@ __global__ __launch_bounds__(kThreads, 2) void ggemm_kernel(GgArgs args) {
     if (tid == 0) s_tiles[0] = 0;
   }
   __syncthreads();
-  const int NT = MODE == kGgGateUp ? (args.N + 63) / 64 : (args.N + BN - 1) / BN;
+  const int NT = (args.N + C::OUT_COLS - 1) / C::OUT_COLS;
   const int mtiles = s_tiles[E];
   const int64_t total = (int64_t)mtiles * NT;
   // XCD-aware remap: workgroups are dispatched round-robin over 8 XCDs, so
@@ -102,163 +178,208 @@ __global__ __launch_bounds__(kThreads, 2) void ggemm_kernel(GgArgs args) {
   const int e = s_expert;
   const int seg0 = args.g.offsets[e], seg1 = args.g.offsets[e + 1];
   const int m0 = seg0 + (mt - s_tiles[e]) * BM;
-  const int n0 = MODE == kGgGateUp ? nt * 64 : nt * BN;
-
-  // ---- loader assignments: thread -> (row, half) ----
-  const int lrow = tid >> 1, lhalf = tid & 1;
-  // A row source
-  const int aj = m0 + lrow;
-  const bool a_ok = aj < seg1;
-  int64_t a_src = 0;
-  if (a_ok) {
-    a_src = MODE == kGgDown ? (int64_t)aj : route_row(args.rm, aj);
-  }
-  const uint16_t* a_ptr = args.x + a_src * args.Kin + lhalf * 32;
-  // B row source
-  const tfm_affine* bm;
-  int bn;
-  if (MODE == kGgGateUp) {
-    bm = lrow < 64 ? &args.wa : &args.wb;
-    bn = n0 + (lrow & 63);
-  } else {
-    bm = &args.wa;
-    bn = n0 + lrow;
-  }
-  const bool b_ok = bn < args.N;
-  const int64_t b_row = (int64_t)e * args.N + (b_ok ? bn : 0);
-  const uint32_t* b_q = bm->q + b_row * (args.Kin / 8) + lhalf * 4;
-  const uint16_t* b_s = static_cast<const uint16_t*>(bm->scales) + b_row * (args.Kin / 64);
-  const uint16_t* b_b = static_cast<const uint16_t*>(bm->biases) + b_row * (args.Kin / 64);
-
+  const int rows_valid = min(BM, seg1 - m0);
+  const int n0 = nt * C::OUT_COLS;
   const int KT = args.Kin / BK;
-  uint4 ra[4];
-  uint4 rb;
-  uint16_t rs = 0, rbias = 0;
 
-  auto gload = [&](int kt) {
-    if (a_ok) {
-      const uint4* p = reinterpret_cast<const uint4*>(a_ptr + kt * BK);
+  // ---- A: global -> LDS copies ----
+  // Wave w fills rows [w*BM/W, (w+1)*BM/W), 8 rows (1 KB) per instruction:
+  // lane l of copy i writes LDS slot l%8 of row w*BM/W + i*8 + l/8, which
+  // under the swizzle holds chunk (l%8) ^ ((row >> 1) & 7).
+  const __amdgpu_buffer_rsrc_t ra = gg_rsrc(args.x, args.x_bytes);
+  const __amdgpu_buffer_rsrc_t rnull = gg_rsrc(args.x, 0);
+  uint32_t a_off[LA];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ra[i] = p[i];
+  for (int i = 0; i < LA; ++i) {
+    const int r = wave * (BM / C::WAVES) + i * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < rows_valid) {
+      const int64_t src = MODE == kGgDown ? (int64_t)(m0 + r) : route_row(args.rm, m0 + r);
+      a_off[i] = (uint32_t)((src * args.Kin + c * 8) * 2);
     } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ra[i] = make_uint4(0, 0, 0, 0);
+      a_off[i] = kOob;
     }
-    if (b_ok) {
-      rb = *reinterpret_cast<const uint4*>(b_q + kt * 8);
-      rs = b_s[kt];
-      rbias = b_b[kt];
-    } else {
-      rb = make_uint4(0, 0, 0, 0);
-      rs = 0;
-      rbias = 0;
+  }
+  // Step kt of A into LDS stage `dst`; steps past the last read zeros.
+  auto a_copy = [&](uint16_t* dst, int kt) {
+    const __amdgpu_buffer_rsrc_t r = kt < KT ? ra : rnull;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) lds_dma16(r, dst + (wave * (BM / C::WAVES) + i * 8) * BK, a_off[i], kt * BK * 2);
+  };
+
+  // ---- B: packed weights ----
+  // Chunk q = i*T + tid -> weight row q/2, half q%2 (32 nibbles). Gate/up
+  // tiles hold BN/2 gate rows then BN/2 up rows.
+  const uint32_t qrow = (uint32_t)args.Kin / 2, srow = (uint32_t)(args.Kin / BK) * 2;
+  __amdgpu_buffer_rsrc_t rbq[LB], rbs[LB], rbb[LB];
+  uint32_t b_qoff[LB], b_soff[LB];
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int qw = i * T + wave * 64;  // first chunk of this wave (uniform)
+    const bool up = MODE == kGgGateUp && (qw >> 1) >= BN / 2;
+    const tfm_affine& bm = up ? args.wb : args.wa;
+    const int q = qw + lane;
+    const int r = q >> 1;
+    const int bn = MODE == kGgGateUp ? n0 + (r & (BN / 2 - 1)) : n0 + r;
+    const size_t ebase = (size_t)e * args.N;
+    rbq[i] = gg_rsrc(reinterpret_cast<const char*>(bm.q) + ebase * qrow, (uint32_t)args.N * qrow);
+    rbs[i] = gg_rsrc(static_cast<const char*>(bm.scales) + ebase * srow, (uint32_t)args.N * srow);
+    rbb[i] = gg_rsrc(static_cast<const char*>(bm.biases) + ebase * srow, (uint32_t)args.N * srow);
+    const bool ok = bn < args.N;
+    b_qoff[i] = ok ? (uint32_t)bn * qrow + (q & 1) * 16 : kOob;
+    b_soff[i] = ok ? (uint32_t)bn * srow : kOob;
+  }
+  auto bload = [&](RawB<LB>& st, int kt) {
+    const bool live = kt < KT;
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      st.b[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[i] : rnull, b_qoff[i], kt * 32, 0));
+      st.s[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbs[i] : rnull, b_soff[i], kt * 2, 0);
+      st.bias[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbb[i] : rnull, b_soff[i], kt * 2, 0);
     }
   };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(&sA[buf][swz(lrow, lhalf * 4 + i)]) = ra[i];
-    const float s = bf2f(rs), b = bf2f(rbias);
-    const uint32_t words[4] = {rb.x, rb.y, rb.z, rb.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float d[8];
-      dequant8(words[i], s, b, d);
-      uint4 pk;
-      pk.x = pack_bf16x2(d[0], d[1]);
-      pk.y = pack_bf16x2(d[2], d[3]);
-      pk.z = pack_bf16x2(d[4], d[5]);
-      pk.w = pack_bf16x2(d[6], d[7]);
-      *reinterpret_cast<uint4*>(&sB[buf][swz(lrow, lhalf * 4 + i)]) = pk;
-    }
+  // Word w (of LB*4) of the dequantised B step.
+  auto bstore_word = [&](const RawB<LB>& st, uint16_t* dst, int w) {
+    const int i = w / 4, k = w % 4;
+    const int q = i * T + tid;
+    const uint4 pk = dequant_word(word_of(st.b[i], k), bf2f((uint16_t)st.s[i]), bf2f((uint16_t)st.bias[i]));
+    *reinterpret_cast<uint4*>(&dst[swz(q >> 1, (q & 1) * 4 + k)]) = pk;
   };
 
   // ---- wave tile ----
-  const int wm = wave >> 1, wn = wave & 1;
-  int brow[2];
-  if (MODE == kGgGateUp) {
-    brow[0] = wn * 32;        // gate columns
-    brow[1] = 64 + wn * 32;   // up columns
-  } else {
-    brow[0] = wn * 64;
-    brow[1] = wn * 64 + 32;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  int brow[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (MODE == kGgGateUp)
+      brow[j] = j < NB / 2 ? wn * (C::WN / 2) + j * 32 : BN / 2 + wn * (C::WN / 2) + (j - NB / 2) * 32;
+    else
+      brow[j] = wn * C::WN + j * 32;
   }
-  f32x16_t acc[2][2];
+
+  f32x16_t acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
+  // MFMAs of one LDS stage (fragments of K sub-step ks+1 are read during the
+  // MFMAs of ks); the dequantised next B step is written during sub-steps
+  // 1..3, so its loads have had more than a step to arrive.
+  auto compute = [&](const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt, uint16_t* nB) {
+    bf16x8_t af[2][MB], bfr[2][NB];
+    auto frag = [&](int ks, int slot) {
+      const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        af[slot][i] = *reinterpret_cast<const bf16x8_t*>(&A[swz(wm * C::WM + i * 32 + (lane & 31), kc)]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        bfr[slot][j] = *reinterpret_cast<const bf16x8_t*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
+    };
+    frag(0, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int kc = ks * 2 + (lane >> 5);
-      bf16x8_t af[2], bfr[2];
+      if (ks < 3) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = wm * 64 + i * 32 + (lane & 31);
-        af[i] = *reinterpret_cast<const bf16x8_t*>(&sA[buf][swz(r, kc)]);
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+      if (ks >= 1) {
+#pragma unroll
+        for (int w = (ks - 1) * LB * 4 / 3; w < ks * LB * 4 / 3; ++w) bstore_word(nxt, nB, w);
       }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = brow[j] + (lane & 31);
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(&sB[buf][swz(r, kc)]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) lstore(buf ^ 1);
-    __syncthreads();
+  };
+  // End of a step: the barrier's release fence waits for this wave's LDS
+  // writes (copies and dequantised B) and its outstanding weight loads; after
+  // it every wave's writes are visible.
+  auto step_end = [&]() { __syncthreads(); };
+
+  // With an odd step count the loop runs one more step on zeros (A and B
+  // both read from null buffers), which adds nothing.
+  RawB<LB> st0, st1;
+  a_copy(sA0, 0);
+  bload(st0, 0);
+  bload(st1, 1);
+#pragma unroll
+  for (int w = 0; w < LB * 4; ++w) bstore_word(st0, sB0, w);
+  step_end();
+  for (int kt = 0; kt < KT; kt += 2) {
+    a_copy(sA1, kt + 1);
+    bload(st0, kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sA0, sB0, st1, sB1);
+    step_end();
+    a_copy(sA0, kt + 2);
+    bload(st1, kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sA1, sB1, st0, sB0);
+    step_end();
   }
 
   // ---- epilogue ----
-  const int col = acc_col(lane);
+  // Private staging block of this wave: 32 rows x SROW bf16 inside one of the
+  // four stages (every wave is past the last barrier, so LDS is free).
+  uint16_t* stage = (wave & 3) == 0 ? sA0 : (wave & 3) == 1 ? sA1 : (wave & 3) == 2 ? sB0 : sB1;
+  stage += (wave >> 2) * 32 * C::SROW;
+  constexpr int CPR = C::WCOLS / 8;             // 16-byte chunks per staged row
+  const int col_base = MODE == kGgGateUp ? n0 + wn * (C::WN / 2) : n0 + wn * C::WN;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < MB; ++i) {
+    const int r0 = wm * C::WM + i * 32;         // first tile row of this block
+    if (r0 >= rows_valid) break;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int j = m0 + wm * 64 + i * 32 + acc_row(v, lane);
-      if (j >= seg1) continue;
+      const int rr = acc_row(v, lane);
       if (MODE == kGgGateUp) {
-        const int n = n0 + wn * 32 + col;
-        if (n < args.N)
-          args.out[(int64_t)j * args.N + n] = f2bf(silu_mul(acc[i][0][v], acc[i][1][v]));
-      } else if (MODE == kGgPlain) {
-        const int64_t orow = args.rm.order[j];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int n = n0 + brow[b] + col;
-          if (n < args.N) args.out[orow * args.N + n] = f2bf(acc[i][b][v]);
-        }
+        for (int jb = 0; jb < NB / 2; ++jb)
+          stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2bf(swiglu(acc[i][jb][v], acc[i][jb + NB / 2][v]));
       } else {
-        const int f = args.g.order[j];
-        const float gw = args.gates ? args.gates[f] : 1.0f;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int n = n0 + brow[b] + col;
-          if (n >= args.N) continue;
-          const float val = acc[i][b][v] * gw;
-          if (args.acc)
-            atomicAdd(&args.acc[(int64_t)(f / args.K) * args.N + n], val);
-          else
-            args.P[(int64_t)j * args.N + n] = val;
-        }
+        for (int jb = 0; jb < NB; ++jb) stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2bf(acc[i][jb][v]);
+      }
+    }
+    // Same-wave LDS accesses complete in order: the reads see the writes.
+#pragma unroll
+    for (int c0 = 0; c0 < 32 * CPR; c0 += 64) {
+      const int c = c0 + lane;
+      const int row = c / CPR, part = c % CPR;
+      const int rr = r0 + row;
+      const int n = col_base + part * 8;
+      if (c < 32 * CPR && rr < rows_valid && n < args.N) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&stage[row * C::SROW + part * 8]);
+        const int j = m0 + rr;
+        const int64_t orow = MODE == kGgPlain ? (int64_t)args.rm.order[j] : (int64_t)j;
+        *reinterpret_cast<uint4*>(&args.out[orow * args.N + n]) = v;
       }
     }
   }
 }
 
-static unsigned grid_for(int64_t n_routes, int E, int NT) {
+// Tile shapes (eight waves each): 256 x 256 (2 x 4 waves of 128 x 64) when
+// the experts hold enough routes to fill 256-row tiles, 128 x 256 (2 x 4
+// waves of 64 x 64) otherwise. TFM_GGEMM_TILE=256 or 128 forces one of them.
+static int tile_override() {
+  static int v = [] {
+    const char* s = std::getenv("TFM_GGEMM_TILE");
+    return s ? std::atoi(s) : 0;
+  }();
+  return v;
+}
+
+static bool use_tall(int64_t n_routes, int E) {
+  const int o = tile_override();
+  if (o == 256) return true;
+  if (o == 128) return false;
+  return n_routes >= (int64_t)E * 384;
+}
+
+static unsigned grid_for(int64_t n_routes, int E, int BM, int NT) {
   const int64_t mt_max = (n_routes + BM - 1) / BM + (n_routes < E ? n_routes : E);
   int64_t total = mt_max * NT;
   // round up to a multiple of 8 so every XCD share is complete
@@ -267,32 +388,51 @@ static unsigned grid_for(int64_t n_routes, int E, int NT) {
   return (unsigned)total;
 }
 
-static void check_shapes(int N, int Kin) {
+template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE>
+static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE>;
+  const int NT = (a.N + C::OUT_COLS - 1) / C::OUT_COLS;
+  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE><<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+}
+
+template <int MODE>
+static void launch_mode(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  if (use_tall(n_routes, E))
+    launch_one<256, 256, 2, 4, MODE>(a, n_routes, E, s);
+  else
+    launch_one<128, 256, 2, 4, MODE>(a, n_routes, E, s);
+}
+
+static void check_shapes(int N, int Kin, int64_t x_rows) {
   if (Kin % BK != 0) fail(TFM_E_UNSUPPORTED, "grouped GEMM: input width must be a multiple of 64");
   if (N % 64 != 0) fail(TFM_E_UNSUPPORTED, "grouped GEMM: output width must be a multiple of 64");
+  // Buffer offsets are 32-bit: activations and one expert's packed weights
+  // must stay below 2 GiB.
+  if ((double)x_rows * Kin * 2 >= 2147483648.0 || (double)N * Kin / 2 >= 2147483648.0)
+    fail(TFM_E_UNSUPPORTED, "grouped GEMM: operand of 2 GiB or more");
 }
 
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         uint16_t* h, float* zero_buf, int64_t zero_count, hipStream_t s) {
+                         uint16_t* h, hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin);
+  check_shapes(N, Kin, rm.nx);
   GgArgs a{};
-  a.x = x; a.rm = rm; a.g = g; a.wa = gate; a.wb = up; a.N = N; a.Kin = Kin;
-  a.out = h; a.zero_buf = zero_buf; a.zero_count = zero_count;
-  ggemm_kernel<kGgGateUp><<<grid_for(n_routes, E, (N + 63) / 64), kThreads, 0, s>>>(a);
+  a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = gate; a.wb = up;
+  a.N = N; a.Kin = Kin; a.out = h;
+  launch_mode<kGgGateUp>(a, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM gate/up launch");
 }
 
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, const float* gates, int K,
-                       float* acc, float* P, hipStream_t s) {
+                       const tfm_affine& w, int N, int Kin, uint16_t* y_sorted, hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin);
+  check_shapes(N, Kin, n_routes);
   GgArgs a{};
-  a.x = hsorted; a.rm = RowMap{g.order, nullptr, K, 0, nullptr}; a.g = g; a.wa = w; a.wb = w; a.N = N;
-  a.Kin = Kin; a.gates = gates; a.K = K; a.acc = acc; a.P = P;
-  ggemm_kernel<kGgDown><<<grid_for(n_routes, E, (N + BN - 1) / BN), kThreads, 0, s>>>(a);
+  a.x = hsorted; a.x_bytes = (uint32_t)(n_routes * Kin * 2);
+  a.rm = RowMap{g.order, nullptr, 1, 0, nullptr}; a.g = g; a.wa = w; a.wb = w; a.N = N;
+  a.Kin = Kin; a.out = y_sorted;
+  launch_mode<kGgDown>(a, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM down launch");
 }
 
@@ -300,10 +440,11 @@ void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t
                         int E, const tfm_affine& w, int N, int Kin, uint16_t* out,
                         hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin);
+  check_shapes(N, Kin, rm.nx);
   GgArgs a{};
-  a.x = x; a.rm = rm; a.g = g; a.wa = w; a.wb = w; a.N = N; a.Kin = Kin; a.out = out;
-  ggemm_kernel<kGgPlain><<<grid_for(n_routes, E, (N + BN - 1) / BN), kThreads, 0, s>>>(a);
+  a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = w; a.wb = w;
+  a.N = N; a.Kin = Kin; a.out = out;
+  launch_mode<kGgPlain>(a, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM plain launch");
 }
 

@@ -67,9 +67,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
       float s = 0.0f;
 #pragma unroll
       for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
-      s = group_sum<64>(s);
+      s = wave_tree_sum64(s);
       const int tok = tt * TW + t;
-      if (lane == 0 && tok < T) {
+      if (lane == 63 && tok < T) {
         const float v = bias ? s + be : s;
         logits[(int64_t)tok * E + e] = f2bf(v);
       }
@@ -91,8 +91,8 @@ __global__ __launch_bounds__(256) void router_logits_generic(const uint16_t* __r
   float s = 0.0f;
   for (int j = 0; j < c; ++j)
     s = __builtin_fmaf(bf2f(x[(int64_t)tok * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
-  s = group_sum<64>(s);
-  if (lane == 0) logits[(int64_t)tok * E + e] = f2bf(bias ? s + bias[e] : s);
+  s = wave_tree_sum64(s);
+  if (lane == 63) logits[(int64_t)tok * E + e] = f2bf(bias ? s + bias[e] : s);
 }
 
 template <int C>
@@ -158,6 +158,54 @@ __global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ 
     idx[(int64_t)t * K + lane] = id;
     if (gates_f32) gates_f32[(int64_t)t * K + lane] = g;
   }
+}
+
+// Top-k of kTopkTokensPerBlock tokens per workgroup (one wave per token at a
+// time), plus the histogram of the workgroup's routes over the E experts for
+// the grouping pass (its chunk is kTopkTokensPerBlock * K flat routes).
+template <int ROUTE>
+__global__ __launch_bounds__(256) void topk_hist_kernel(const uint16_t* __restrict__ logits, int T,
+                                                        int E, int K, int32_t* __restrict__ idx,
+                                                        float* __restrict__ gates_f32,
+                                                        int32_t* __restrict__ hist) {
+  __shared__ int h[65];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid <= E) h[tid] = 0;
+  __syncthreads();
+  constexpr int kPerWave = kTopkTokensPerBlock / 4;
+  for (int i = 0; i < kPerWave; ++i) {
+    const int t = blockIdx.x * kTopkTokensPerBlock + wave * kPerWave + i;
+    if (t >= T) break;  // wave-uniform
+    const uint16_t* row = logits + (int64_t)t * E;
+    float g;
+    int id;
+    if (ROUTE == TFM_ROUTE_OLMOE) {
+      uint16_t gb;
+      id = olmoe_route_wave(row, E, K, &g, &gb);
+    } else {
+      id = granite_route_wave(row, E, K, &g);
+    }
+    if (lane < K) {
+      idx[(int64_t)t * K + lane] = id;
+      gates_f32[(int64_t)t * K + lane] = g;
+      atomicAdd(&h[id], 1);
+    }
+  }
+  __syncthreads();
+  if (tid <= E) hist[(int64_t)blockIdx.x * (E + 1) + tid] = h[tid];
+}
+
+void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                      float* gates_f32, int32_t* hist, hipStream_t s) {
+  if (T <= 0) return;
+  const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
+  if (route_kind == TFM_ROUTE_OLMOE)
+    topk_hist_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+  else
+    topk_hist_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+  check_hip(hipGetLastError(), "topk_hist launch");
 }
 
 void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,

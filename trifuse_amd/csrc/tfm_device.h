@@ -70,6 +70,29 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// The same pairwise tree as group_sum<64> (lanes l and l^1 first, then pairs
+// of pairs), computed with DPP instead of LDS shuffles; the root lands in lane
+// 63. Each level adds the two operands group_sum<64> adds (after level 2 the
+// lanes of a quad, after level 3 of a half-row, hold equal values, so the
+// mirror patterns pick the same partner sums as xor 4 and xor 8, and row_bcast
+// 15/31 deliver the xor 16/32 partners to the last row), and IEEE addition is
+// commutative, so the result is bit-identical.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_plus(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+  return v + __int_as_float(s);
+}
+
+__device__ __forceinline__ float wave_tree_sum64(float v) {
+  v = dpp_plus<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]  (xor 1)
+  v = dpp_plus<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]  (xor 2)
+  v = dpp_plus<0x141, 0xf>(v);  // row_half_mirror      (xor 4)
+  v = dpp_plus<0x140, 0xf>(v);  // row_mirror           (xor 8)
+  v = dpp_plus<0x142, 0xa>(v);  // row_bcast:15         (xor 16, rows 1 and 3)
+  v = dpp_plus<0x143, 0xc>(v);  // row_bcast:31         (xor 32, rows 2 and 3)
+  return v;                     // lane 63: the tree root
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
@@ -77,7 +100,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // 8 nibbles of a packed word (LSB first) dequantised as s*q+b, as floats.
 // q order: element i is bits [4i, 4i+4).
 __device__ __forceinline__ void dequant8(uint32_t w, float s, float b, float* out) {
-  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  // Opaque to the optimiser, so that the byte extractions below are not
+  // folded into 4-bit field extracts: each converts with one v_cvt_f32_ubyteN.
+  asm("" : "+v"(lo));
+  asm("" : "+v"(hi));
   out[0] = __builtin_fmaf(s, (float)(lo & 0xffu), b);
   out[1] = __builtin_fmaf(s, (float)(hi & 0xffu), b);
   out[2] = __builtin_fmaf(s, (float)((lo >> 8) & 0xffu), b);

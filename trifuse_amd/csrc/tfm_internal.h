@@ -59,9 +59,18 @@ void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, in
 void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
                       hipStream_t s);
 void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
-// Grouping; also zeroes `zero_words` words at `zero` (counters of a later kernel).
-void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, uint32_t* status,
-                  hipStream_t s, uint32_t* zero = nullptr, int zero_words = 0);
+// Grouping (group.hip): per-chunk expert histograms, then a stable scatter.
+// hist holds group_blocks(n, chunk) rows of E+1 counts (bucket E: bad ids).
+constexpr int kGroupChunk = 512;           // routes per chunk for given routes
+constexpr int kTopkTokensPerBlock = 16;    // tokens per top-k workgroup (chunk = 16*K)
+int group_blocks(int64_t n, int chunk);
+void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, int32_t* hist, uint32_t* status,
+                  hipStream_t s);
+void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, const int32_t* hist,
+                          Grouping g, uint32_t* status, hipStream_t s);
+// Top-k that also writes the chunk histograms (chunk = kTopkTokensPerBlock * K routes).
+void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                      float* gates_f32, int32_t* hist, hipStream_t s);
 
 // Decode path (decode.hip), T*K <= 256 routes.
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
@@ -106,32 +115,33 @@ void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_acti
                         int64_t routes, const tfm_affine& w, int N, int Kin, const float* gates,
                         float* P, hipStream_t s);
 
-// Prefill-style grouped GEMM (dequant to LDS bf16, MFMA).
+// Grouped GEMM on expert-contiguous routes (prefill):
 //   gateup: h[j, :] = bf16(silu(x W_gate^T) * (x W_up^T)) for sorted routes j
-//   down:   acc[tok(j), :] += gate_j * (h[j, :] W_down^T)   (fp32 atomics), or
-//           P[j, :] = gate_j * (h[j, :] W_down^T)           (deterministic)
-//   plain:  out[order[j], :] = bf16(x W^T)                  (gather_qmm)
+//   down:   y[j, :] = bf16(h[j, :] W_down^T)             (expert output, sorted j)
+//   plain:  out[order[j], :] = bf16(x W^T)                 (gather_qmm)
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         uint16_t* h, float* zero_buf, int64_t zero_count, hipStream_t s);
+                         uint16_t* h, hipStream_t s);
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, const float* gates, int K,
-                       float* acc, float* P, hipStream_t s);
+                       const tfm_affine& w, int N, int Kin, uint16_t* y_sorted, hipStream_t s);
 void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                         int E, const tfm_affine& w, int N, int Kin, uint16_t* out,
                         hipStream_t s);
 
-// Combine: y[t, c] = bf16(residual[t, c] + rm * sum_k P[inverse[t*K+k], c]) (k ascending)
+// Combine of gate-weighted fp32 rows (decode path):
+//   y[t, c] = bf16(residual[t, c] + rm * sum_k P[inverse[t*K+k], c])   (k ascending)
 // Routes whose sorted position is >= *n_valid (bad expert ids) contribute 0.
 void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
                            int K, int H, const uint16_t* residual, float rmul, uint16_t* y,
                            hipStream_t s);
-// Finalize: y[t, c] = bf16(residual[t, c] + rm * acc[t, c])
-void launch_finalize_acc(const float* acc, int T, int H, const uint16_t* residual, float rmul,
-                         uint16_t* y, hipStream_t s);
-// Expert-sorted output rows for the hook: out[j, c] = bf16(P[j, c])
+// Combine of bf16 expert-output rows (prefill path):
+//   y[t, c] = bf16(residual[t, c] + rm * sum_k gate[t*K+k] * Y[inverse[t*K+k], c])
+// with the same k order and bad-route rule.
+void launch_combine_rows(const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
+                         const float* gates, int T, int K, int H, const uint16_t* residual,
+                         float rmul, uint16_t* y, hipStream_t s);
+// Expert-sorted output rows for the hook (decode path): out[j, c] = bf16(P[j, c])
 void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s);
-void launch_fill_f32(float* p, int64_t n, float v, hipStream_t s);
 void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s);
 void launch_gates_to_f32(int dtype_native_bf16, const void* src, float* dst, int64_t n,
                          hipStream_t s);
