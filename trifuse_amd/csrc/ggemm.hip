@@ -268,7 +268,12 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   // MFMAs of one LDS stage (fragments of K sub-step ks+1 are read during the
   // MFMAs of ks); the dequantised next B step is written during sub-steps
   // 1..3, so its loads have had more than a step to arrive.
-  auto compute = [&](const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt, uint16_t* nB) {
+  // LIVE = false (every row of the wave past the segment): the wave skips
+  // fragment reads and MFMAs, which frees its SIMD's matrix pipe for the
+  // other wave there, and only does its share of the loads and LDS writes.
+  auto compute = [&](auto live_tag, const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt,
+                     uint16_t* nB) {
+    constexpr bool LIVE = decltype(live_tag)::value;
     bf16x8_t af[2][MB], bfr[2][NB];
     auto frag = [&](int ks, int slot) {
       const int kc = ks * 2 + (lane >> 5);
@@ -279,15 +284,17 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
       for (int j = 0; j < NB; ++j)
         bfr[slot][j] = *reinterpret_cast<const bf16x8_t*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
     };
-    frag(0, 0);
+    if constexpr (LIVE) frag(0, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      if (ks < 3) frag(ks + 1, (ks + 1) & 1);
+      if constexpr (LIVE) {
+        if (ks < 3) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+        for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < NB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+      }
       if (ks >= 1) {
 #pragma unroll
         for (int w = (ks - 1) * LB * 4 / 3; w < ks * LB * 4 / 3; ++w) bstore_word(nxt, nB, w);
@@ -308,18 +315,25 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
 #pragma unroll
   for (int w = 0; w < LB * 4; ++w) bstore_word(st0, sB0, w);
   step_end();
-  for (int kt = 0; kt < KT; kt += 2) {
-    a_copy(sA1, kt + 1);
-    bload(st0, kt + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sA0, sB0, st1, sB1);
-    step_end();
-    a_copy(sA0, kt + 2);
-    bload(st1, kt + 3);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(sA1, sB1, st0, sB0);
-    step_end();
-  }
+  auto main_loop = [&](auto live_tag) {
+    for (int kt = 0; kt < KT; kt += 2) {
+      a_copy(sA1, kt + 1);
+      bload(st0, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(live_tag, sA0, sB0, st1, sB1);
+      step_end();
+      a_copy(sA0, kt + 2);
+      bload(st1, kt + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(live_tag, sA1, sB1, st0, sB0);
+      step_end();
+    }
+  };
+  const bool wave_live = wm * C::WM < rows_valid;
+  if (wave_live)
+    main_loop(std::true_type{});
+  else
+    main_loop(std::false_type{});
 
   // ---- epilogue ----
   // Private staging block of this wave: 32 rows x SROW bf16 inside one of the
