@@ -518,13 +518,21 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
                                      reinterpret_cast<int32_t*>(gates_out), R, s);
       return;
     }
+    bool fused_route;
     {
+      // Router linear, top-k and chunk histograms in one kernel where the
+      // hidden size has a variant; otherwise logits then top-k.
       StageScope st(TFM_STAGE_ROUTER, s);
-      launch_router_logits(static_cast<const uint16_t*>(x),
-                           static_cast<const uint16_t*>(weights->router), weights->logit_bias,
-                           (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+      fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
+                                       static_cast<const uint16_t*>(weights->router),
+                                       weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
+                                       ws.hist, nullptr, s);
+      if (!fused_route)
+        launch_router_logits(static_cast<const uint16_t*>(x),
+                             static_cast<const uint16_t*>(weights->router), weights->logit_bias,
+                             (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
     }
-    {
+    if (!fused_route) {
       StageScope st(TFM_STAGE_TOPK, s);
       launch_topk_hist(g.route, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
     }

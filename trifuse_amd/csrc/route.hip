@@ -77,6 +77,138 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
   }
 }
 
+// Prefill routing in one pass: router linear, top-k and the chunk histogram
+// for the grouping. A workgroup takes kTopkTokensPerBlock (4) tokens: every
+// wave keeps their x rows in registers and computes the logits of one
+// quarter of the experts, streaming those router rows (the next one loading
+// while the current one is used), each logit exactly as router_logits_kernel
+// computes it. Then wave t ranks token t from the logits in LDS with the same
+// wave-level ranking as topk_kernel.
+template <int C, int ROUTE>
+__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          const float* __restrict__ bias, int T,
+                                                          int H, int E, int K,
+                                                          int32_t* __restrict__ idx,
+                                                          float* __restrict__ gates_f32,
+                                                          int32_t* __restrict__ hist,
+                                                          uint16_t* __restrict__ logits_out) {
+  constexpr int TB = kTopkTokensPerBlock;
+  static_assert(TB == 4, "one ranking wave per token");
+  __shared__ uint16_t s_logit[TB][64];
+  __shared__ int h[65];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid <= E) h[tid] = 0;
+  const int t0 = blockIdx.x * TB;
+  float xv[TB][C];
+#pragma unroll
+  for (int t = 0; t < TB; ++t) {
+    if (t0 + t < T) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + (int64_t)(t0 + t) * H + lane * C);
+#pragma unroll
+      for (int i = 0; i < C / 8; ++i) {
+        const uint4 v = src[i];
+        xv[t][8 * i + 0] = lo_bf(v.x); xv[t][8 * i + 1] = hi_bf(v.x);
+        xv[t][8 * i + 2] = lo_bf(v.y); xv[t][8 * i + 3] = hi_bf(v.y);
+        xv[t][8 * i + 4] = lo_bf(v.z); xv[t][8 * i + 5] = hi_bf(v.z);
+        xv[t][8 * i + 6] = lo_bf(v.w); xv[t][8 * i + 7] = hi_bf(v.w);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C; ++j) xv[t][j] = 0.0f;
+    }
+  }
+  auto wrow = [&](uint4 (&r)[C / 8], int e) {
+    const uint4* src = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
+#pragma unroll
+    for (int i = 0; i < C / 8; ++i) r[i] = src[i];
+  };
+  auto logits_of = [&](const uint4 (&r)[C / 8], int e) {
+    float wv[C];
+#pragma unroll
+    for (int i = 0; i < C / 8; ++i) {
+      wv[8 * i + 0] = lo_bf(r[i].x); wv[8 * i + 1] = hi_bf(r[i].x);
+      wv[8 * i + 2] = lo_bf(r[i].y); wv[8 * i + 3] = hi_bf(r[i].y);
+      wv[8 * i + 4] = lo_bf(r[i].z); wv[8 * i + 5] = hi_bf(r[i].z);
+      wv[8 * i + 6] = lo_bf(r[i].w); wv[8 * i + 7] = hi_bf(r[i].w);
+    }
+    const float be = bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
+      s = wave_tree_sum64(s);
+      if (lane == 63) s_logit[t][e] = f2bf(bias ? s + be : s);
+    }
+  };
+  const int epw = (E + 3) / 4;
+  const int e0 = wave * epw, e1 = min(E, e0 + epw);
+  if (e0 < e1) {  // wave-uniform
+    uint4 ra[C / 8], rb[C / 8];
+    wrow(ra, e0);
+    for (int e = e0; e < e1; e += 2) {
+      if (e + 1 < e1) wrow(rb, e + 1);
+      logits_of(ra, e);
+      if (e + 1 >= e1) break;
+      if (e + 2 < e1) wrow(ra, e + 2);
+      logits_of(rb, e + 1);
+    }
+  }
+  __syncthreads();  // every expert's logits of the block's tokens are in LDS
+  const int tok = t0 + wave;
+  if (tok < T) {  // wave-uniform
+    const uint16_t* row = &s_logit[wave][0];
+    if (logits_out && lane < E) logits_out[(int64_t)tok * E + lane] = row[lane];
+    float g;
+    int id;
+    if (ROUTE == TFM_ROUTE_OLMOE) {
+      uint16_t gb;
+      id = olmoe_route_wave(row, E, K, &g, &gb);
+    } else {
+      id = granite_route_wave(row, E, K, &g);
+    }
+    if (lane < K) {
+      idx[(int64_t)tok * K + lane] = id;
+      gates_f32[(int64_t)tok * K + lane] = g;
+      atomicAdd(&h[id], 1);
+    }
+  }
+  __syncthreads();
+  if (tid <= E) hist[(int64_t)blockIdx.x * (E + 1) + tid] = h[tid];
+}
+
+template <int C>
+static void launch_router_topk_c(int route_kind, const uint16_t* x, const uint16_t* w,
+                                 const float* bias, int T, int H, int E, int K, int32_t* idx,
+                                 float* gates_f32, int32_t* hist, uint16_t* logits_out,
+                                 hipStream_t s) {
+  const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
+  if (route_kind == TFM_ROUTE_OLMOE)
+    router_topk_kernel<C, TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                 hist, logits_out);
+  else
+    router_topk_kernel<C, TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                   hist, logits_out);
+}
+
+bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
+                        int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
+                        uint16_t* logits_out, hipStream_t s) {
+  if (T <= 0) return true;
+  switch (H) {
+    case 512: launch_router_topk_c<8>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 1024: launch_router_topk_c<16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 1536: launch_router_topk_c<24>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 2048: launch_router_topk_c<32>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    default: return false;
+  }
+  check_hip(hipGetLastError(), "router_topk launch");
+  return true;
+}
+
 // Any H % 64 == 0: the same arithmetic with scalar loads.
 __global__ __launch_bounds__(256) void router_logits_generic(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ w,

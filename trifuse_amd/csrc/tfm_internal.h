@@ -62,13 +62,20 @@ void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs,
 // Grouping (group.hip): per-chunk expert histograms, then a stable scatter.
 // hist holds group_blocks(n, chunk) rows of E+1 counts (bucket E: bad ids).
 constexpr int kGroupChunk = 512;           // routes per chunk for given routes
-constexpr int kTopkTokensPerBlock = 16;    // tokens per top-k workgroup (chunk = 16*K)
+constexpr int kTopkTokensPerBlock = 4;     // tokens per routing workgroup (chunk = 4*K)
 int group_blocks(int64_t n, int chunk);
 void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, int32_t* hist, uint32_t* status,
                   hipStream_t s);
-void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, const int32_t* hist,
+// Scatter with chunk histograms already built (overwritten by chunk bases).
+void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, int32_t* hist,
                           Grouping g, uint32_t* status, hipStream_t s);
 // Top-k that also writes the chunk histograms (chunk = kTopkTokensPerBlock * K routes).
+// Prefill routing in one kernel: logits (optionally written out), top-k and
+// the chunk histogram of kTopkTokensPerBlock tokens per chunk. Returns false
+// (nothing launched) for a hidden size it has no variant for.
+bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
+                        int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
+                        uint16_t* logits_out, hipStream_t s);
 void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
                       float* gates_f32, int32_t* hist, hipStream_t s);
 
