@@ -5,9 +5,10 @@
 //   1. decode_route_kernel: one workgroup per token computes the token's E
 //      router logits (same arithmetic as the router kernel) and its top-k,
 //   2. decode_gateup_kernel: every workgroup first groups the T*K routes by
-//      expert (stable, in LDS; a few hundred VALU ops) and then runs the
-//      gate/up dequant GEMV with the SwiGLU epilogue for its expert and rows;
-//      workgroup (0,0) also publishes the grouping for the next kernels,
+//      expert (stable, in LDS; a few hundred VALU ops) and then streams a few
+//      gate/up row units of one active expert through the dequant GEMV with
+//      the SwiGLU epilogue; workgroup (0, 0) also publishes the grouping for
+//      the next kernels,
 //   3. the down dequant GEMV scaled by each route's gate (gemv.hip),
 //   4. the ordered K reduction + residual (combine.hip).
 // Each kernel boundary is the only synchronisation: on MI355X a launch costs
@@ -25,7 +26,7 @@ constexpr int kDecodeMaxRoutes = 256;  // one thread per route in the grouping
 struct DecodeGateUpArgs {
   const uint16_t* x;       // [T, H]
   const int32_t* idx;      // [R] route -> expert (from decode_route_kernel)
-  int T, E, K, H, I, nit;
+  int T, E, K, H, I;
   tfm_affine gate, up;
   int32_t* order;          // [R] sorted position -> flat route
   int32_t* inverse;        // [R]
@@ -42,7 +43,6 @@ __device__ __forceinline__ uint64_t lanemask_lt64() {
 
 template <int LG>
 __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) {
-  constexpr int RPL = 64 / LG;
   __shared__ GemvLds L;
   __shared__ int s_order[kDecodeMaxRoutes];
   __shared__ int s_off[65];
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
   }
   __syncthreads();
 
-  // Workgroup (0,0) publishes the grouping for the down GEMV and the combine.
+  // Workgroup (0, 0) publishes the grouping for the down GEMV and the combine.
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     if (live) {
       A.order[pos] = tid;
@@ -114,12 +114,10 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
     if (tid == 0) *A.status = 0u;
   }
 
-  // Gate/up rows of this workgroup's expert.
-  const int a = blockIdx.y;
-  if (a >= s_act[E]) return;
-  const int ex = s_act[a];
-  const int wrow0 = (blockIdx.x * 4 + wave) * A.nit * RPL;
+  // Gate/up rows: kGemvUnits row units of active expert blockIdx.y.
   const int N = A.I;
+  if ((int)blockIdx.y >= s_act[E]) return;
+  const int ex = s_act[blockIdx.y];
   uint16_t* h = A.h;
   auto xrow = [&](int j) -> int64_t { return (int64_t)(s_order[j] / K); };
   auto stage = [&](int, int) {};
@@ -127,8 +125,8 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
     const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
     h[(int64_t)j * N + n] = f2bf(hv);
   };
-  gemv_expert_rows<LG, 2>(L, A.x, A.H, N, A.gate, A.up, ex, s_off[ex], s_off[ex + 1], A.nit, wrow0,
-                          xrow, stage, emit);
+  gemv_units<LG, 2, kGemvUnits>(L, A.x, A.H, N, A.gate, A.up, ex, s_off[ex], s_off[ex + 1],
+                                blockIdx.x * kGemvUnits, xrow, stage, emit);
 }
 
 // Router logits and top-k of one token per workgroup (16 waves). Logit e is
@@ -281,13 +279,13 @@ void launch_decode_gateup(const uint16_t* x, const int32_t* idx, int T, int E, i
   if (T * K > kDecodeMaxRoutes) fail(TFM_E_INVALID, "decode gate/up: more than 256 routes");
   if (H % 64 != 0 || H > 2048) fail(TFM_E_UNSUPPORTED, "decode gate/up: hidden width above 2048");
   DecodeGateUpArgs A{};
-  A.x = x; A.idx = idx; A.T = T; A.E = E; A.K = K; A.H = H; A.I = I; A.nit = kGemvRowLoads;
+  A.x = x; A.idx = idx; A.T = T; A.E = E; A.K = K; A.H = H; A.I = I;
   A.gate = gate; A.up = up; A.order = g.order; A.inverse = g.inverse; A.offsets = g.offsets;
   A.active = g.active; A.h = h; A.status = status;
   const int lg = lg_for(H);
-  const int rows_per_block = 4 * A.nit * (64 / lg);
+  const int ur = 4 * (64 / lg), upe = (I + ur - 1) / ur;
   const int max_active = T * K < E ? T * K : E;
-  dim3 grid((unsigned)((I + rows_per_block - 1) / rows_per_block), (unsigned)max_active);
+  const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active);
   switch (lg) {
     case 4: decode_gateup_kernel<4><<<grid, 256, 0, s>>>(A); break;
     case 8: decode_gateup_kernel<8><<<grid, 256, 0, s>>>(A); break;

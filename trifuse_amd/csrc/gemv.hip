@@ -17,30 +17,27 @@
 // chunk sums. The kernel is VALU-bound at decode shapes (about 7 VALU ops to
 // unpack 8 nibbles plus 4 dot2 per route), so instructions per weight byte are
 // what the layout minimises.
+#include <cstdlib>
+
 #include "gemv_body.h"
 
 namespace tfm {
 
 // Standalone decode GEMV over grouped routes (gather_qmm and the MoE block
-// given routes): block = 4 waves on one routed expert (blockIdx.y indexes the
-// ascending active-expert list) and a contiguous range of rows (blockIdx.x).
+// given routes): workgroup (bx, a) (4 waves) streams kGemvUnits row units of
+// active expert a (blockIdx.y indexes the ascending active-expert list).
 template <int LG, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x, RowMap rm,
                                                    Grouping g, tfm_affine wa, tfm_affine wb,
-                                                   int N, int kin, int nit,
-                                                   const float* __restrict__ gates,
+                                                   int N, int kin, const float* __restrict__ gates,
                                                    void* __restrict__ out) {
   constexpr int NM = MODE == kGateUp ? 2 : 1;
-  constexpr int RPL = 64 / LG;
   __shared__ GemvLds L;
   __shared__ float xgate[kGemvXB];
   __shared__ int xorow[kGemvXB];
-  const int a = blockIdx.y;
   const int E = g.E;
-  if (a >= g.active[E]) return;
-  const int e = g.active[a];
-  const int wave = threadIdx.x >> 6;
-  const int wrow0 = (blockIdx.x * 4 + wave) * nit * RPL;
+  if ((int)blockIdx.y >= g.active[E]) return;
+  const int e = g.active[blockIdx.y];
   auto xrow = [&](int j) -> int64_t { return MODE == kScaled ? (int64_t)j : route_row(rm, j); };
   auto stage = [&](int jb, int nb) {
     const int t = threadIdx.x;
@@ -59,8 +56,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
       static_cast<float*>(out)[(int64_t)j * N + n] = a0 * xgate[t];
     }
   };
-  gemv_expert_rows<LG, NM>(L, x, kin, N, wa, wb, e, g.offsets[e], g.offsets[e + 1], nit, wrow0,
-                           xrow, stage, emit);
+  gemv_units<LG, NM, kGemvUnits>(L, x, kin, N, wa, wb, e, g.offsets[e], g.offsets[e + 1],
+                                 blockIdx.x * kGemvUnits, xrow, stage, emit);
 }
 
 template <int MODE>
@@ -71,12 +68,11 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   if (Kin % 64 != 0 || Kin <= 0 || Kin > 2048)
     fail(TFM_E_UNSUPPORTED, "affine GEMV: input width must be a multiple of 64 up to 2048");
   const int nch = Kin / 32;
-  const int nit = kGemvRowLoads;
-#define TFM_GEMV_LAUNCH(LGV)                                                                  \
+#define TFM_GEMV_LAUNCH(LGV)                                                                \
   {                                                                                         \
-    const int rows_per_block = 4 * nit * (64 / LGV);                                          \
-    dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)max_active);  \
-    gemv_kernel<LGV, MODE><<<grid, 256, 0, s>>>(x, rm, g, wa, wb, N, Kin, nit, gates, out);   \
+    const int ur = 4 * (64 / LGV), upe = (N + ur - 1) / ur;                                 \
+    const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active); \
+    gemv_kernel<LGV, MODE><<<grid, 256, 0, s>>>(x, rm, g, wa, wb, N, Kin, gates, out);      \
   }
   if (nch <= 4) TFM_GEMV_LAUNCH(4)
   else if (nch <= 8) TFM_GEMV_LAUNCH(8)

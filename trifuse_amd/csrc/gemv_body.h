@@ -99,40 +99,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-constexpr int kGemvXB = 4;  // routes staged per LDS batch
-// Row-loads per wave: enough workgroups to fill the chip for a handful of
-// routed experts, little per-workgroup setup relative to the weights read.
-constexpr int kGemvRowLoads = 2;
+constexpr int kGemvXB = 4;     // routes staged per LDS batch
+// Row units (one row-load per wave each) per workgroup, all of one expert:
+// many short workgroups in flight measured faster at decode shapes than
+// fewer, longer ones (deeper register prefetch costs occupancy).
+constexpr int kGemvUnits = 2;
 
-// LDS of the row loop: the staged x chunks of up to kGemvXB routes.
+// LDS of the row units: the staged x chunks of up to kGemvXB routes.
 struct GemvLds {
   uint4 xs[kGemvXB][4][64];  // [route][quarter][chunk]: 16 pair-dwords per chunk
   float xsum[kGemvXB][64];
 };
 
-// The row loop of one routed expert. The calling workgroup (4 waves) covers
-// rows [wave_row0, wave_row0 + nit*RPL) per wave (wave_row0 already includes
-// the wave), for routes [j0, j1) of expert `e` of matrices wa (and wb for
-// gate/up, NM = 2).
+// Row units of one routed expert. The rows of an expert are cut into units
+// of UR = 4 * (64 / LG) rows (one row-load per wave); the calling workgroup
+// (4 waves) processes units [rc0, rc0 + NU) (those below N rows) for routes
+// [j0, j1) of expert e of matrices wa (and wb for gate/up, NM = 2). Every
+// row-load is issued before the x staging, so their memory latencies overlap
+// each other and the staging's.
 //   xrow(j)            row of x feeding route j
 //   stage(jb, nb)      called by every thread before the batch barrier, to
 //                      stage per-route data of routes [jb, jb+nb)
 //   emit(j, t, n, a0, a1)  called by the lane holding row n's totals for route
 //                      j (batch slot t); a1 = a0 unless NM = 2.
 // Every thread of the workgroup must call it (it contains barriers).
-template <int LG, int NM, typename XRow, typename Stage, typename Emit>
-__device__ __forceinline__ void gemv_expert_rows(GemvLds& L, const uint16_t* __restrict__ x, int kin,
-                                                 int N, const tfm_affine& wa, const tfm_affine& wb,
-                                                 int e, int j0, int j1, int nit, int wave_row0,
-                                                 XRow xrow, Stage stage, Emit emit) {
+template <int LG, int NM, int NU, typename XRow, typename Stage, typename Emit>
+__device__ __forceinline__ void gemv_units(GemvLds& L, const uint16_t* __restrict__ x, int kin, int N,
+                                           const tfm_affine& wa, const tfm_affine& wb, int e, int j0,
+                                           int j1, int rc0, XRow xrow, Stage stage, Emit emit) {
   constexpr int RPL = 64 / LG;
+  constexpr int UR = 4 * RPL;
   const int nch = kin / 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int sub = lane / LG, ll = lane % LG;
   const bool lane_ok = ll < nch;
-
   const uint32_t qrow = (uint32_t)kin / 2, srow = (uint32_t)kin / 32;  // bytes per row
+
   __amdgpu_buffer_rsrc_t rq[NM], rs[NM], rb[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
@@ -141,13 +145,15 @@ __device__ __forceinline__ void gemv_expert_rows(GemvLds& L, const uint16_t* __r
     rs[m] = make_rsrc(static_cast<const char*>(mm.scales) + (size_t)e * N * srow, (uint32_t)N * srow);
     rb[m] = make_rsrc(static_cast<const char*>(mm.biases) + (size_t)e * N * srow, (uint32_t)N * srow);
   }
-  // Lanes past the row's chunks read far out of range (zeros).
-  const uint32_t qoff0 = ll < nch ? (uint32_t)(wave_row0 + sub) * qrow + 16u * ll : 0x7ff00000u;
-  const uint32_t soff0 = (uint32_t)(wave_row0 + sub) * srow + 2u * (ll >> 1);
-
-  auto load = [&](int it, RawW (&w)[NM]) {
-    const uint32_t qo = qoff0 + (uint32_t)(it * RPL) * qrow;
-    const uint32_t so = soff0 + (uint32_t)(it * RPL) * srow;
+  // Row of this lane in unit u: rc0*UR + u*UR + wave*RPL + sub. Lanes past the
+  // row's chunks read far out of range (zeros); rows past N are out of range
+  // of the expert's buffer (zeros).
+  const int n0 = rc0 * UR + wave * RPL + sub;
+  const uint32_t qoff0 = lane_ok ? (uint32_t)n0 * qrow + 16u * ll : 0x7ff00000u;
+  const uint32_t soff0 = (uint32_t)n0 * srow + 2u * (ll >> 1);
+  auto load = [&](int u, RawW (&w)[NM]) {
+    const uint32_t qo = qoff0 + (uint32_t)(u * UR) * qrow;
+    const uint32_t so = soff0 + (uint32_t)(u * UR) * srow;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       w[m].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[m], qo, 0, 0));
@@ -158,9 +164,10 @@ __device__ __forceinline__ void gemv_expert_rows(GemvLds& L, const uint16_t* __r
 
   for (int jb = j0; jb < j1; jb += kGemvXB) {
     const int nb = min(kGemvXB, j1 - jb);
-    RawW cur[NM];
-    if (nit > 0) load(0, cur);
-    if (jb != j0) __syncthreads();
+    RawW w[NU][NM];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) load(u, w[u]);
+    if (jb != j0) __syncthreads();  // every wave is done with the previous staging
     for (int p = tid; p < nb * nch; p += 256) {
       const int t = p / nch, c = p % nch;
       ChunkX cx;
@@ -172,48 +179,56 @@ __device__ __forceinline__ void gemv_expert_rows(GemvLds& L, const uint16_t* __r
     }
     stage(jb, nb);
     __syncthreads();
-#pragma unroll 1
-    for (int it = 0; it < nit; ++it) {
-      RawW nxt[NM];
-      if (it + 1 < nit) load(it + 1, nxt);
-      uint32_t qp[NM][16];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const RawW (&cur)[NM] = w[u];
       float sc[NM], cc[NM];
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        unpack_word(cur[m].q.x, &qp[m][0]);
-        unpack_word(cur[m].q.y, &qp[m][4]);
-        unpack_word(cur[m].q.z, &qp[m][8]);
-        unpack_word(cur[m].q.w, &qp[m][12]);
         sc[m] = bf2f((uint16_t)cur[m].s);
         cc[m] = __builtin_fmaf(-128.0f, sc[m], bf2f((uint16_t)cur[m].b));
       }
-      const int n = wave_row0 + it * RPL + sub;
-#pragma unroll 1
-      for (int t = 0; t < nb; ++t) {
-        uint32_t xp[16];
+      // One packed word at a time: its (128+q) pairs for every matrix, then
+      // their dot products with the staged x of every route of the batch.
+      float d0[kGemvXB][NM], d1[kGemvXB][NM];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint4 v = L.xs[t][q][ll];
-          xp[4 * q] = v.x; xp[4 * q + 1] = v.y; xp[4 * q + 2] = v.z; xp[4 * q + 3] = v.w;
-        }
-        const float xsm = L.xsum[t][ll];
-        float acc[NM];
+      for (int t = 0; t < kGemvXB; ++t)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          float d0 = 0.0f, d1 = 0.0f;
+        for (int m = 0; m < NM; ++m) d0[t][m] = d1[t][m] = 0.0f;
 #pragma unroll
-          for (int k = 0; k < 16; k += 2) {
-            d0 = dot2(qp[m][k], xp[k], d0);
-            d1 = dot2(qp[m][k + 1], xp[k + 1], d1);
+      for (int q = 0; q < 4; ++q) {
+        uint32_t qp[NM][4];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) unpack_word(word_of(cur[m].q, q), qp[m]);
+#pragma unroll
+        for (int t = 0; t < kGemvXB; ++t) {
+          if (t < nb) {
+            const uint4 v = L.xs[t][q][ll];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+              d0[t][m] = dot2(qp[m][0], v.x, d0[t][m]);
+              d1[t][m] = dot2(qp[m][1], v.y, d1[t][m]);
+              d0[t][m] = dot2(qp[m][2], v.z, d0[t][m]);
+              d1[t][m] = dot2(qp[m][3], v.w, d1[t][m]);
+            }
           }
-          // Lanes past the row's chunks (kin < 32 * LG) contribute nothing; their
-          // staged x is stale, so they are masked rather than multiplied by 0.
-          acc[m] = dpp_group_sum<LG>(lane_ok ? __builtin_fmaf(sc[m], d0 + d1, cc[m] * xsm) : 0.0f);
         }
-        if (group_sum_lane<LG>(lane) && n < N) emit(jb + t, t, n, acc[0], acc[NM - 1]);
       }
+      const int n = n0 + u * UR;
 #pragma unroll
-      for (int m = 0; m < NM; ++m) cur[m] = nxt[m];
+      for (int t = 0; t < kGemvXB; ++t) {
+        if (t < nb) {
+          const float xsm = L.xsum[t][ll];
+          float acc[NM];
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+            // Lanes past the row's chunks (kin < 32 * LG) contribute nothing;
+            // their staged x is stale, so they are masked rather than
+            // multiplied by 0.
+            acc[m] = dpp_group_sum<LG>(lane_ok ? __builtin_fmaf(sc[m], d0[t][m] + d1[t][m], cc[m] * xsm) : 0.0f);
+          if (group_sum_lane<LG>(lane) && n < N) emit(jb + t, t, n, acc[0], acc[NM - 1]);
+        }
+      }
     }
   }
 }

@@ -78,10 +78,6 @@ __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
   return pk;
 }
 
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int k) {
-  return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
-}
-
 // silu(g) * u with the hardware exp and reciprocal (relative error ~1e-7,
 // far below the bf16 rounding that follows).
 __device__ __forceinline__ float swiglu(float g, float u) {
