@@ -52,7 +52,8 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="measure the headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--deterministic", action="store_true", help="ordered K reduction in prefill")
+    p.add_argument("--deterministic", action="store_true",
+                   help="pass TFM_FLAG_DETERMINISTIC (every path already reduces routes in k order)")
     return p.parse_args()
 
 
@@ -217,8 +218,8 @@ def measured_traffic(workload: str):
 
 def cpu_baseline(r: Runner, seconds: float):
     """The oracle's MLX-semantics CPU block on the host cores over a bounded
-    sample: whole layers of the same workload (first layers first) until
-    `seconds` have elapsed, at least one."""
+    sample: whole layers of the same workload, cycling through its layers,
+    until `seconds` have elapsed (at least one layer)."""
     import numpy as np
 
     import oracle
@@ -235,13 +236,22 @@ def cpu_baseline(r: Runner, seconds: float):
     class NpLayer:
         pass
 
-    for lay in r.layers[:r.wl.layers]:
+    def host_layer(lay):
         nl = NpLayer()
         for name in ("gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q", "down_s", "down_b"):
             t = getattr(lay, name).cpu()
             setattr(nl, name, t.numpy() if t.dtype == r.torch.int32 else t.view(r.torch.int16).numpy())
         router = lay.router.cpu().view(r.torch.int16).numpy()
         lb = None if lay.logit_bias is None else lay.logit_bias.cpu().numpy()
+        return nl, router, lb
+
+    host = {}
+    nsrc = r.wl.layers
+    while True:
+        li = layers % nsrc
+        if li not in host:
+            host[li] = host_layer(r.layers[li])
+        nl, router, lb = host[li]
         t0 = time.perf_counter()
         _, _, _, used = oracle.moe_block_cpu(x, nl, r.geom.route, router, lb, top_k=r.geom.top_k,
                                              threads=threads)
@@ -251,7 +261,8 @@ def cpu_baseline(r: Runner, seconds: float):
         if elapsed >= seconds:
             break
     return {"value": done_tokens / elapsed, "unit": "tok/s", "cores": used, "kind": "port",
-            "sample": f"{layers} layer(s) x {T} tokens of {r.wl.name}, "
+            "sample": f"{layers} layer pass(es) x {T} tokens of {r.wl.name} (cycling over its "
+                      f"{min(layers, nsrc)} distinct layer(s)), "
                       f"{elapsed:.1f} s, {used} OpenMP threads on {model}",
             "per_layer_ms": elapsed / layers * 1e3}
 

@@ -92,15 +92,15 @@ def test_olmoe_prefill_t4096_zipf(gpu):
     top4 = np.sort(counts)[::-1][:4].sum() / counts.sum()
     log(f"  top-4 expert share {top4:.3f}, hottest expert {counts.max()} routes")
     assert 0.30 < top4 < 0.50
-    # Deterministic mode: bit-identical on a second run, and equal in value to the
-    # atomic mode within the block tolerance.
+    # Every path reduces a token's K routes in k order: a second run, with or
+    # without the deterministic flag and on a fresh block, is bit-identical.
     blk = _block(w.geometry)
     wts = tmoe.ExpertWeights.from_layer(layer)
     y1 = blk.forward(x.to(gpu), wts, deterministic=True)
     y2 = blk.forward(x.to(gpu), wts, deterministic=True)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
-    assert max_rel(f32(y1), f32(y)) <= BLOCK_TOL
+    assert torch.equal(y1, y)
 
 
 def test_granite_prefill_then_decode(gpu):
