@@ -18,6 +18,11 @@ reported under "per_workload". Each reports per-layer latency, tok/s, the
 algorithmic bytes (routed experts counted from the step's own routing) and
 FLOPs, and its roofline fraction (HBM for decode, bf16 MFMA for prefill).
 
+Each workload also reports the step replayed from a HIP graph
+(graph_per_layer_us: the GPU-side time without per-launch host work; the
+replayed output is checked bit for bit against the eager one). `value` is the
+eager (non-graph) rate.
+
 "roofline" is for the dominant kernel of the headline workload, timed with HIP
 events around each of its launches on the stream it runs on. "cpu_baseline"
 is the oracle's MLX-semantics CPU block on the host cores over a bounded
@@ -126,6 +131,39 @@ class Runner:
         wall = time.perf_counter() - t0
         return start.elapsed_time(end) / steps, wall * 1e3 / steps
 
+    def graph_time(self, steps, warmup):
+        """The step captured once in a HIP graph (torch.cuda.CUDAGraph) and
+        replayed: the GPU-side step time without per-launch host work.
+        Returns (ms per step, replayed output == eager output bit for bit)."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step()  # warm the allocator on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.step()
+        y_graph = self.y  # written by every replay
+        self.step()
+        torch.cuda.synchronize()
+        y_eager = self.y.clone()
+        for _ in range(max(1, warmup)):
+            graph.replay()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(y_graph, y_eager))
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        del graph
+        return ms, same
+
     def stage_times(self, steps):
         from trifuse_amd.moe import StageProfiler
 
@@ -143,7 +181,7 @@ class Runner:
         return out
 
 
-def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages):
+def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages, graph=None):
     from trifuse_amd import workload as wl
 
     g, T, L = r.geom, r.wl.tokens, r.nlayers
@@ -168,6 +206,11 @@ def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages):
         "bound": bound,
         "stages_us": {k: round(v["us_per_launch"], 3) for k, v in stages.items()},
     }
+    if graph is not None:
+        gms, same = graph
+        rep["graph_per_layer_us"] = gms / L * 1e3
+        rep["graph_tok_per_s"] = T * L / (gms * 1e-3)
+        rep["graph_matches_eager"] = same
     return rep
 
 
@@ -287,7 +330,8 @@ def main():
     ms, wall = head.time_steps(args.steps, args.warmup)
     log(f"[bench] {args.workload}: {ms * 1e3:.1f} us/step")
     stages = head.stage_times(max(10, min(args.steps, 100)))
-    report = workload_report(head, ms, wall, stages)
+    graph = head.graph_time(args.steps, args.warmup)
+    report = workload_report(head, ms, wall, stages, graph)
     roof = dominant_roofline(head, stages)
     roof["traffic"] = measured_traffic(args.workload)
 
@@ -303,7 +347,8 @@ def main():
             steps = args.steps if name in DECODE else max(20, args.steps // 4)
             m, wa = r.time_steps(steps, max(3, args.warmup // 2))
             st = r.stage_times(10)
-            per[name] = workload_report(r, m, wa, st)
+            gr = r.graph_time(steps, max(3, args.warmup // 2))
+            per[name] = workload_report(r, m, wa, st, gr)
             per[name]["roofline_gateup"] = dominant_roofline(r, st)
             if not args.no_cpu and name in ("olmoe_prefill_t4096_zipf", "olmoe_decode_t1"):
                 per[name]["cpu_baseline"] = cpu_baseline(r, 3.0)

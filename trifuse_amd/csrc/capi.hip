@@ -117,8 +117,10 @@ struct BlockWs {
   float* gates;
   Grouping grp;
   uint16_t* h;
-  float* P;  // [R, H] sorted rows; the atomic path uses its start as acc [T, H]
+  float* P;  // [R, H] sorted rows (fp32 in decode, bf16 expert outputs in prefill)
   int32_t* hist;  // grouping chunk histograms
+  int4* slots;    // decode: per active slot {expert, first route, end route, 0}
+  float* gates_sorted;  // decode: gates in sorted order
   size_t bytes;
 };
 
@@ -140,6 +142,8 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   const int64_t chunks = std::max<int64_t>(group_blocks(R, kGroupChunk),
                                            group_blocks(R, kTopkTokensPerBlock * g.experts_per_token));
   w.hist = c.take<int32_t>((size_t)((chunks + 1) * (g.num_experts + 1)));
+  w.slots = c.take<int4>((size_t)g.num_experts);
+  w.gates_sorted = c.take<float>((size_t)R);
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -495,17 +499,22 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
         StageScope st(TFM_STAGE_ROUTER, s);
         launch_decode_route(g.route, static_cast<const uint16_t*>(x),
                             static_cast<const uint16_t*>(weights->router), weights->logit_bias, T,
-                            H, E, K, nullptr, ws.idx, ws.gates, s);
+                            H, E, K, ws.logits, ws.idx, ws.gates, s);
       }
+      // The gate/up kernel publishes the grouping with its slot table and
+      // sorted gates for the down GEMV.
+      Grouping gd = ws.grp;
+      gd.slots = ws.slots;
+      gd.gates_sorted = ws.gates_sorted;
       {
         StageScope st(TFM_STAGE_GATEUP, s);
-        launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, T, E, K, H, I, weights->gate,
-                             weights->up, ws.grp, ws.h, &ws.hdr->status, s);
+        launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
+                             weights->gate, weights->up, gd, ws.h, &ws.hdr->status, s);
       }
       const int max_active = (int)(R < E ? R : E);
       {
         StageScope st(TFM_STAGE_DOWN, s);
-        launch_gemv_scaled(ws.h, ws.grp, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
+        launch_gemv_scaled(ws.h, gd, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
       }
       {
         StageScope st(TFM_STAGE_COMBINE, s);

@@ -12,7 +12,11 @@
 
 namespace tfm {
 
-// 8 columns per thread; H % 8 == 0.
+// 8 columns per thread; H % 8 == 0. For K <= KMAX every route's row index and
+// then every row is requested before the first is used (rows of bad routes
+// read row 0 and are dropped by a select), so a thread waits for memory
+// twice rather than twice per route; larger K takes the plain loop.
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __restrict__ P,
                                                              const int32_t* __restrict__ inverse,
                                                              const int32_t* __restrict__ n_valid,
@@ -27,13 +31,35 @@ __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __rest
 #pragma unroll
   for (int v = 0; v < 8; ++v) s[v] = 0.0f;
   const int nv = *n_valid;
-  for (int k = 0; k < K; ++k) {
-    const int64_t row = inverse[(int64_t)t * K + k];
-    if (row >= nv) continue;
-    const float4* p = reinterpret_cast<const float4*>(P + row * H + c);
-    const float4 a = p[0], b = p[1];
-    s[0] += a.x; s[1] += a.y; s[2] += a.z; s[3] += a.w;
-    s[4] += b.x; s[5] += b.y; s[6] += b.z; s[7] += b.w;
+  if (K <= KMAX) {
+    int row[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) row[k] = k < K ? inverse[(int64_t)t * K + k] : nv;
+    float4 a[KMAX], b[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int64_t r = row[k] < nv ? row[k] : 0;
+      const float4* p = reinterpret_cast<const float4*>(P + r * H + c);
+      a[k] = p[0];
+      b[k] = p[1];
+    }
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const bool on = row[k] < nv;
+      s[0] = on ? s[0] + a[k].x : s[0]; s[1] = on ? s[1] + a[k].y : s[1];
+      s[2] = on ? s[2] + a[k].z : s[2]; s[3] = on ? s[3] + a[k].w : s[3];
+      s[4] = on ? s[4] + b[k].x : s[4]; s[5] = on ? s[5] + b[k].y : s[5];
+      s[6] = on ? s[6] + b[k].z : s[6]; s[7] = on ? s[7] + b[k].w : s[7];
+    }
+  } else {
+    for (int k = 0; k < K; ++k) {
+      const int64_t row = inverse[(int64_t)t * K + k];
+      if (row >= nv) continue;
+      const float4* p = reinterpret_cast<const float4*>(P + row * H + c);
+      const float4 a = p[0], b = p[1];
+      s[0] += a.x; s[1] += a.y; s[2] += a.z; s[3] += a.w;
+      s[4] += b.x; s[5] += b.y; s[6] += b.z; s[7] += b.w;
+    }
   }
   float r[8];
   if (residual) {
@@ -57,8 +83,8 @@ void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t
                            hipStream_t s) {
   if (T <= 0) return;
   const int64_t n = (int64_t)T * (H / 8);
-  combine_sorted_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, inverse, n_valid, T, K, H,
-                                                                   residual, rmul, y);
+  combine_sorted_kernel<8><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, inverse, n_valid, T, K, H,
+                                                                      residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 

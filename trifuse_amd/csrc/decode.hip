@@ -1,9 +1,10 @@
 // Decode path of the MoE block (few routes: T*K <= 256).
 //
 // The block that NativeGraniteMoEPrefill::moe runs per layer
-// (MLXNativeGraniteMoEPrefill.h:627-702) as four kernels:
-//   1. decode_route_kernel: one workgroup per token computes the token's E
-//      router logits (same arithmetic as the router kernel) and its top-k,
+// (MLXNativeGraniteMoEPrefill.h:627-702) as five kernels:
+//   1. decode_logits_kernel: one workgroup per expert computes that expert's
+//      router logit for every token (same arithmetic as the router kernel),
+//      then topk_kernel ranks each token's E logits,
 //   2. decode_gateup_kernel: every workgroup first groups the T*K routes by
 //      expert (stable, in LDS; a few hundred VALU ops) and then streams a few
 //      gate/up row units of one active expert through the dequant GEMV with
@@ -15,7 +16,6 @@
 // ~2.4 us, while a cross-workgroup hand-off inside a kernel needs an L2
 // write-back per workgroup, which costs more at these grid sizes.
 #include "gemv_body.h"
-#include "route_wave.h"
 #include "tfm_device.h"
 #include "tfm_internal.h"
 
@@ -26,12 +26,15 @@ constexpr int kDecodeMaxRoutes = 256;  // one thread per route in the grouping
 struct DecodeGateUpArgs {
   const uint16_t* x;       // [T, H]
   const int32_t* idx;      // [R] route -> expert (from decode_route_kernel)
+  const float* gates;      // [R] route gates (fp32, flat order)
   int T, E, K, H, I;
   tfm_affine gate, up;
   int32_t* order;          // [R] sorted position -> flat route
   int32_t* inverse;        // [R]
   int32_t* offsets;        // [E+1]
   int32_t* active;         // [E+1]
+  int4* slots;             // [E] per active slot {expert, first route, end route, 0}
+  float* gates_sorted;     // [R] gates in sorted order
   uint16_t* h;             // [R, I] SwiGLU output, expert-sorted rows
   uint32_t* status;        // the call's status word, cleared here
 };
@@ -60,6 +63,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
   (&wcnt[0][0])[tid] = 0;
   const bool live = tid < R;
   const int e = live ? A.idx[tid] : 0;
+  const float gate = (live && blockIdx.x == 0 && blockIdx.y == 0) ? A.gates[tid] : 0.0f;
   __syncthreads();
   uint64_t match = __ballot(live);
 #pragma unroll
@@ -106,10 +110,15 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
     if (live) {
       A.order[pos] = tid;
       A.inverse[tid] = pos;
+      A.gates_sorted[pos] = gate;
     }
     if (tid <= E) {
       A.offsets[tid] = s_off[tid];
       if (tid == E || tid < s_act[E]) A.active[tid] = s_act[tid];
+    }
+    if (tid < E) {
+      const int ex = tid < s_act[E] ? s_act[tid] : -1;
+      A.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, 0) : make_int4(ex, s_off[ex], s_off[ex + 1], 0);
     }
     if (tid == 0) *A.status = 0u;
   }
@@ -129,109 +138,87 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
                                 blockIdx.x * kGemvUnits, xrow, stage, emit);
 }
 
-// Router logits and top-k of one token per workgroup (16 waves). Logit e is
-// computed by one wave exactly as the router kernel does (lane l sums x*w
-// over its H/64 contiguous elements with sequential fused multiply-adds, then
-// the xor-shuffle tree across lanes, then + bias, rounded to bf16); wave 0
-// then ranks the E logits of the token.
-template <int C, int ROUTE>
-__global__ __launch_bounds__(1024) void decode_route_kernel(const uint16_t* __restrict__ x,
+// Router logits of the decode path, one workgroup (4 waves) per expert e:
+// logit[t][e] for every token t, each computed exactly as the router kernel
+// does (lane l sums x*w over its H/64 contiguous elements with sequential
+// fused multiply-adds, then the xor-shuffle tree across lanes, then + bias,
+// rounded to bf16). One router row per workgroup spreads the router read
+// over E compute units (a single compute unit pulling the whole router is
+// limited by its own outstanding misses). Wave w takes tokens w, w + 4, ..,
+// two at a time.
+template <int C>
+__global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
-                                                            const float* __restrict__ bias,
-                                                            int H, int E, int K,
-                                                            uint16_t* __restrict__ logits,
-                                                            int32_t* __restrict__ idx,
-                                                            float* __restrict__ gates) {
-  __shared__ uint16_t s_logit[64];
-  const int t = blockIdx.x;
+                                                            const float* __restrict__ bias, int T,
+                                                            int H, int E,
+                                                            uint16_t* __restrict__ logits) {
+  const int e = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  float xv[C];
-  const uint4* xs = reinterpret_cast<const uint4*>(x + (int64_t)t * H + lane * C);
+  float wv[C];
+  const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
 #pragma unroll
   for (int i = 0; i < C / 8; ++i) {
-    const uint4 v = xs[i];
-    xv[8 * i + 0] = lo_bf(v.x); xv[8 * i + 1] = hi_bf(v.x);
-    xv[8 * i + 2] = lo_bf(v.y); xv[8 * i + 3] = hi_bf(v.y);
-    xv[8 * i + 4] = lo_bf(v.z); xv[8 * i + 5] = hi_bf(v.z);
-    xv[8 * i + 6] = lo_bf(v.w); xv[8 * i + 7] = hi_bf(v.w);
+    const uint4 v = ws[i];
+    wv[8 * i + 0] = lo_bf(v.x); wv[8 * i + 1] = hi_bf(v.x);
+    wv[8 * i + 2] = lo_bf(v.y); wv[8 * i + 3] = hi_bf(v.y);
+    wv[8 * i + 4] = lo_bf(v.z); wv[8 * i + 5] = hi_bf(v.z);
+    wv[8 * i + 6] = lo_bf(v.w); wv[8 * i + 7] = hi_bf(v.w);
   }
-  for (int e = wave; e < E; e += 16) {
-    const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
-    float s = 0.0f;
+  const float be = bias ? bias[e] : 0.0f;
+  // Token rows past T read zeros (offset beyond the buffer).
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)T * H * 2), 0x00020000);
+  for (int t0 = wave; t0 < T; t0 += 8) {
+    uint4 xv[2][C / 8];
 #pragma unroll
-    for (int i = 0; i < C / 8; ++i) {
-      const uint4 v = ws[i];
-      s = __builtin_fmaf(xv[8 * i + 0], lo_bf(v.x), s);
-      s = __builtin_fmaf(xv[8 * i + 1], hi_bf(v.x), s);
-      s = __builtin_fmaf(xv[8 * i + 2], lo_bf(v.y), s);
-      s = __builtin_fmaf(xv[8 * i + 3], hi_bf(v.y), s);
-      s = __builtin_fmaf(xv[8 * i + 4], lo_bf(v.z), s);
-      s = __builtin_fmaf(xv[8 * i + 5], hi_bf(v.z), s);
-      s = __builtin_fmaf(xv[8 * i + 6], lo_bf(v.w), s);
-      s = __builtin_fmaf(xv[8 * i + 7], hi_bf(v.w), s);
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + 4 * u;
+      const uint32_t off = t < T ? ((uint32_t)t * H + lane * C) * 2u : 0x80000000u;
+#pragma unroll
+      for (int i = 0; i < C / 8; ++i)
+        xv[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16u * i, 0, 0));
     }
-    s = wave_tree_sum64(s);
-    if (lane == 63) {
-      const uint16_t lb = f2bf(bias ? s + bias[e] : s);
-      s_logit[e] = lb;
-      if (logits) logits[(int64_t)t * E + e] = lb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + 4 * u;
+      if (t < T) {  // wave-uniform
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < C / 8; ++i) {
+          const uint4 v = xv[u][i];
+          s = __builtin_fmaf(lo_bf(v.x), wv[8 * i + 0], s);
+          s = __builtin_fmaf(hi_bf(v.x), wv[8 * i + 1], s);
+          s = __builtin_fmaf(lo_bf(v.y), wv[8 * i + 2], s);
+          s = __builtin_fmaf(hi_bf(v.y), wv[8 * i + 3], s);
+          s = __builtin_fmaf(lo_bf(v.z), wv[8 * i + 4], s);
+          s = __builtin_fmaf(hi_bf(v.z), wv[8 * i + 5], s);
+          s = __builtin_fmaf(lo_bf(v.w), wv[8 * i + 6], s);
+          s = __builtin_fmaf(hi_bf(v.w), wv[8 * i + 7], s);
+        }
+        s = wave_tree_sum64(s);
+        if (lane == 63) logits[(int64_t)t * E + e] = f2bf(bias ? s + be : s);
+      }
     }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  float g;
-  int id;
-  if (ROUTE == TFM_ROUTE_OLMOE) {
-    uint16_t gb;
-    id = olmoe_route_wave(s_logit, E, K, &g, &gb);
-  } else {
-    id = granite_route_wave(s_logit, E, K, &g);
-  }
-  if (lane < K) {
-    idx[(int64_t)t * K + lane] = id;
-    gates[(int64_t)t * K + lane] = g;
   }
 }
 
-// Any H % 64 == 0: the same arithmetic as decode_route_kernel with scalar loads.
-template <int ROUTE>
-__global__ __launch_bounds__(1024) void decode_route_generic(const uint16_t* __restrict__ x,
+// Any H % 64 == 0: the same arithmetic as decode_logits_kernel with scalar loads.
+__global__ __launch_bounds__(256) void decode_logits_generic(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ w,
-                                                             const float* __restrict__ bias,
-                                                             int H, int E, int K,
-                                                             uint16_t* __restrict__ logits,
-                                                             int32_t* __restrict__ idx,
-                                                             float* __restrict__ gates) {
-  __shared__ uint16_t s_logit[64];
-  const int t = blockIdx.x;
+                                                             const float* __restrict__ bias, int T,
+                                                             int H, int E,
+                                                             uint16_t* __restrict__ logits) {
+  const int e = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = H / 64;
-  for (int e = wave; e < E; e += 16) {
+  for (int t = wave; t < T; t += 4) {
     float s = 0.0f;
     for (int j = 0; j < c; ++j)
       s = __builtin_fmaf(bf2f(x[(int64_t)t * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
     s = wave_tree_sum64(s);
-    if (lane == 63) {
-      const uint16_t lb = f2bf(bias ? s + bias[e] : s);
-      s_logit[e] = lb;
-      if (logits) logits[(int64_t)t * E + e] = lb;
-    }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  float g;
-  int id;
-  if (ROUTE == TFM_ROUTE_OLMOE) {
-    uint16_t gb;
-    id = olmoe_route_wave(s_logit, E, K, &g, &gb);
-  } else {
-    id = granite_route_wave(s_logit, E, K, &g);
-  }
-  if (lane < K) {
-    idx[(int64_t)t * K + lane] = id;
-    gates[(int64_t)t * K + lane] = g;
+    if (lane == 63) logits[(int64_t)t * E + e] = f2bf(bias ? s + bias[e] : s);
   }
 }
 
@@ -245,41 +232,27 @@ void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* rout
                          hipStream_t s) {
   if (T <= 0) return;
   if (E > 64) fail(TFM_E_UNSUPPORTED, "decode routing: more than 64 experts");
-#define TFM_DR(CV)                                                                            \
-  {                                                                                         \
-    if (route_kind == TFM_ROUTE_OLMOE)                                                       \
-      decode_route_kernel<CV, TFM_ROUTE_OLMOE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K,   \
-                                                                  logits, idx, gates);        \
-    else                                                                                    \
-      decode_route_kernel<CV, TFM_ROUTE_GRANITE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K, \
-                                                                    logits, idx, gates);      \
-  }
+  if (!logits) fail(TFM_E_INVALID, "decode routing: logits buffer missing");
   switch (H) {
-    case 512: TFM_DR(8) break;
-    case 1024: TFM_DR(16) break;
-    case 1536: TFM_DR(24) break;
-    case 2048: TFM_DR(32) break;
-    case 3072: TFM_DR(48) break;
-    case 4096: TFM_DR(64) break;
-    default:
-      if (route_kind == TFM_ROUTE_OLMOE)
-        decode_route_generic<TFM_ROUTE_OLMOE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K, logits,
-                                                                 idx, gates);
-      else
-        decode_route_generic<TFM_ROUTE_GRANITE><<<T, 1024, 0, s>>>(x, router, bias, H, E, K,
-                                                                   logits, idx, gates);
+    case 512: decode_logits_kernel<8><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1024: decode_logits_kernel<16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1536: decode_logits_kernel<24><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 2048: decode_logits_kernel<32><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    default: decode_logits_generic<<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
   }
-#undef TFM_DR
-  check_hip(hipGetLastError(), "decode route launch");
+  check_hip(hipGetLastError(), "decode logits launch");
+  launch_topk(route_kind, logits, T, E, K, idx, nullptr, gates, s);
 }
 
-void launch_decode_gateup(const uint16_t* x, const int32_t* idx, int T, int E, int K, int H, int I,
-                          const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
-                          uint16_t* h, uint32_t* status, hipStream_t s) {
+void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
+                          int K, int H, int I, const tfm_affine& gate, const tfm_affine& up,
+                          const Grouping& g, uint16_t* h, uint32_t* status, hipStream_t s) {
+  if (!g.slots || !g.gates_sorted) fail(TFM_E_INVALID, "decode gate/up: slot table missing");
   if (T * K > kDecodeMaxRoutes) fail(TFM_E_INVALID, "decode gate/up: more than 256 routes");
   if (H % 64 != 0 || H > 2048) fail(TFM_E_UNSUPPORTED, "decode gate/up: hidden width above 2048");
   DecodeGateUpArgs A{};
-  A.x = x; A.idx = idx; A.T = T; A.E = E; A.K = K; A.H = H; A.I = I;
+  A.x = x; A.idx = idx; A.gates = gates; A.T = T; A.E = E; A.K = K; A.H = H; A.I = I;
+  A.slots = g.slots; A.gates_sorted = g.gates_sorted;
   A.gate = gate; A.up = up; A.order = g.order; A.inverse = g.inverse; A.offsets = g.offsets;
   A.active = g.active; A.h = h; A.status = status;
   const int lg = lg_for(H);

@@ -35,14 +35,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   __shared__ GemvLds L;
   __shared__ float xgate[kGemvXB];
   __shared__ int xorow[kGemvXB];
-  const int E = g.E;
-  if ((int)blockIdx.y >= g.active[E]) return;
-  const int e = g.active[blockIdx.y];
+  // Expert and route range of slot blockIdx.y: one read of the slot table
+  // where the decode gate/up kernel wrote it, else active list then offsets.
+  int e, j0, j1;
+  if (g.slots) {
+    const int4 sl = g.slots[blockIdx.y];
+    if (sl.x < 0) return;
+    e = sl.x;
+    j0 = sl.y;
+    j1 = sl.z;
+  } else {
+    if ((int)blockIdx.y >= g.active[g.E]) return;
+    e = g.active[blockIdx.y];
+    j0 = g.offsets[e];
+    j1 = g.offsets[e + 1];
+  }
   auto xrow = [&](int j) -> int64_t { return MODE == kScaled ? (int64_t)j : route_row(rm, j); };
   auto stage = [&](int jb, int nb) {
     const int t = threadIdx.x;
     if (t < nb) {
-      if (MODE == kScaled) xgate[t] = gates ? gates[rm.order[jb + t]] : 1.0f;
+      if (MODE == kScaled)
+        xgate[t] = g.gates_sorted ? g.gates_sorted[jb + t] : gates ? gates[rm.order[jb + t]] : 1.0f;
       if (MODE == kPlain) xorow[t] = rm.order[jb + t];
     }
   };
@@ -56,8 +69,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
       static_cast<float*>(out)[(int64_t)j * N + n] = a0 * xgate[t];
     }
   };
-  gemv_units<LG, NM, kGemvUnits>(L, x, kin, N, wa, wb, e, g.offsets[e], g.offsets[e + 1],
-                                 blockIdx.x * kGemvUnits, xrow, stage, emit);
+  gemv_units<LG, NM, kGemvUnits>(L, x, kin, N, wa, wb, e, j0, j1, blockIdx.x * kGemvUnits, xrow, stage,
+                                 emit);
 }
 
 template <int MODE>

@@ -17,10 +17,10 @@ __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint
 // Round to nearest even, NaN kept quiet with its sign. Integer arithmetic, so
 // the result does not depend on the hardware denormal mode.
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x0040u;  // NaN: keep sign and payload, set the quiet bit
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 // Two floats to packed bf16 (low = a), hardware round-to-nearest-even.

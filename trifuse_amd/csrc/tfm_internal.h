@@ -49,6 +49,12 @@ struct Grouping {
   int32_t* offsets;  // [E+1]
   int32_t* active;   // [E+1] ids of experts with routes, ascending; active[E] = count
   int E;             // number of experts
+  // Written by the decode gate/up kernel for the decode down GEMV (null on
+  // other paths): per active slot s {expert, first route, end route, 0}
+  // (slots past the active count hold expert -1), and the route gates in
+  // sorted order.
+  int4* slots;          // [E]
+  float* gates_sorted;  // [n]
 };
 
 // ---- launchers (defined in the .hip files) ----
@@ -83,9 +89,11 @@ void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int 
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s);
-void launch_decode_gateup(const uint16_t* x, const int32_t* idx, int T, int E, int K, int H, int I,
-                          const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
-                          uint16_t* h, uint32_t* status, hipStream_t s);
+// Also publishes the grouping (g, including g.slots and g.gates_sorted from
+// the flat fp32 `gates`).
+void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
+                          int K, int H, int I, const tfm_affine& gate, const tfm_affine& up,
+                          const Grouping& g, uint16_t* h, uint32_t* status, hipStream_t s);
 
 // Row source of a sorted route j: x row = x_rows ? x_rows[order[j]] : order[j] / K.
 // Rows outside [0, nx) are read as row 0 and flag TFM_STATUS_BAD_ROW_INDEX.

@@ -24,7 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
-from typing import Optional, Tuple
+from typing import Dict, Optional, Tuple
 
 import torch
 
@@ -287,6 +287,8 @@ class MoEBlock:
         self._lib = lib
         self._plan = handle
         self._ws: Optional[torch.Tensor] = None
+        self._ws_bytes: Dict[int, int] = {}
+        self._wcache: Dict[Tuple[int, bool], tuple] = {}
 
     def close(self) -> None:
         if getattr(self, "_plan", None):
@@ -301,7 +303,11 @@ class MoEBlock:
 
     # -- workspace ---------------------------------------------------------
     def workspace_bytes(self, tokens: int) -> int:
-        return int(self._lib.tfm_workspace_bytes(self._plan, tokens))
+        n = self._ws_bytes.get(tokens)
+        if n is None:
+            n = int(self._lib.tfm_workspace_bytes(self._plan, tokens))
+            self._ws_bytes[tokens] = n
+        return n
 
     def workspace(self, tokens: int, device) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
@@ -325,7 +331,24 @@ class MoEBlock:
             raise ValueError("hidden width differs")
         return x.numel() // self.hidden_size
 
+    _WEIGHT_FIELDS = ("router", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q",
+                      "down_s", "down_b", "logit_bias")
+
     def _weights(self, w: ExpertWeights, router: bool) -> MoeWeights:
+        """Validated C-ABI weight struct of `w`, cached per weights object while
+        its tensors keep their storage (a decode step calls this once per layer)."""
+        key = (id(w), router)
+        ptrs = tuple(0 if t is None else t.data_ptr() for t in (getattr(w, f) for f in self._WEIGHT_FIELDS))
+        hit = self._wcache.get(key)
+        if hit is not None and hit[0] is w and hit[1] == ptrs:
+            return hit[2]
+        mw = self._build_weights(w, router)
+        if len(self._wcache) >= 64:
+            self._wcache.clear()
+        self._wcache[key] = (w, ptrs, mw)
+        return mw
+
+    def _build_weights(self, w: ExpertWeights, router: bool) -> MoeWeights:
         H, I, E = self.hidden_size, self.intermediate_size, self.num_experts
         g = 64
         shapes = {
