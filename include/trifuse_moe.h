@@ -190,6 +190,21 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens,
                     int32_t* idx_out, float* gates_out, uint32_t flags,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* The block with its neighbouring step fused in, as the reference layer runs
+ * it (MLXNativeGraniteMoEPrefill.h:485-487):
+ *   post = rms_norm(h, norm_weight, eps)          (fast::rms_norm, :485)
+ *   y    = h + rm * sum_k gate_k * expert_k(post)   (moe(post, h, ...), :486, :688-701)
+ * h, y: [T, H] in the plan dtype, y must not alias h; norm_weight: [H] in the
+ * plan dtype. The RMSNorm order is bit-defined: lane l of 64 sums x*x over
+ * its H/64 contiguous elements with sequential fma, a pairwise tree over
+ * the lanes, mean = sum / H, inv = 1 / sqrt(mean + eps), then
+ * post = round(w * round(h * inv)). Same workspace, outputs and flags as
+ * tfm_moe_forward. */
+int tfm_moe_forward_rmsnorm(const tfm_plan* plan, const void* h, int64_t tokens,
+                            const void* norm_weight, float eps, const tfm_moe_weights* weights,
+                            void* y, int32_t* idx_out, float* gates_out, uint32_t flags,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* NativeMoEExpertHook::GPUCallable (MLXMoEExpertHook.h:23-30,
  * MLXNativeGraniteMoEPrefill.h:635-658): for N parallel routes
  * (token_indices[i], expert_ids[i]) compute the expert outputs in expert-sorted
@@ -214,7 +229,8 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
 #define TFM_STAGE_GATEUP 3  /* gate/up expert matmuls + SwiGLU              */
 #define TFM_STAGE_DOWN 4    /* down expert matmul (+ gate weighting)        */
 #define TFM_STAGE_COMBINE 5 /* K reduction + residual                       */
-#define TFM_STAGE_COUNT 6
+#define TFM_STAGE_NORM 6    /* post-attention RMSNorm (forward_rmsnorm)    */
+#define TFM_STAGE_COUNT 7
 
 /* Host-wall stage timing in the spirit of TriFuse's TRIFUSE_PREFILL_TIMING
  * stage lines (patches/executorch.patch:307-322), measured on the GPU: while

@@ -99,6 +99,15 @@ def router_logits(x, w, bias=None) -> np.ndarray:
     return out
 
 
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """Post-attention RMSNorm (bf16 in and out), bit-defined order (oracle.h)."""
+    x, w = _u16(x), _u16(w)
+    T, H = x.shape
+    out = np.empty((T, H), dtype=np.uint16)
+    load().orc_rmsnorm(_p(x), _p(w), c_float(eps), c_int(T), c_int(H), _p(out))
+    return out
+
+
 def olmoe_softmax(logits) -> np.ndarray:
     lg = _u16(logits)
     T, E = lg.shape

@@ -92,6 +92,28 @@ void orc_router_logits(const uint16_t* x, const uint16_t* w, const float* bias,
   }
 }
 
+void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out) {
+  const int c = H / 64;
+  float lane[64];
+  for (int t = 0; t < T; ++t) {
+    const uint16_t* xr = x + (int64_t)t * H;
+    for (int l = 0; l < 64; ++l) {
+      float s = 0.0f;
+      for (int j = 0; j < c; ++j) {
+        const float v = orc_bf16_to_f32(xr[l * c + j]);
+        s = fmaf(v, v, s);
+      }
+      lane[l] = s;
+    }
+    const float mean = tree64(lane) / (float)H;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int h = 0; h < H; ++h) {
+      const float nx = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(xr[h]) * inv));
+      out[(int64_t)t * H + h] = orc_f32_to_bf16(orc_bf16_to_f32(w[h]) * nx);
+    }
+  }
+}
+
 /* Softmax normaliser in the reference's shape (MLXOLMoERouter.h:46-58):
  * four consecutive values summed in order, then a tree over the (up to 16)
  * four-value chunks; here the tree is the natural pairwise one, with absent

@@ -46,6 +46,16 @@ void orc_expf_array(const float* in, float* out, int64_t n);
 void orc_router_logits(const uint16_t* x, const uint16_t* w, const float* bias,
                        int T, int H, int E, uint16_t* logits);
 
+/* Post-attention RMSNorm in the layer's dtype (MLXNativeGraniteMoEPrefill.h:
+ * 485, fast::rms_norm(h, post_norm, eps)), with this build's bit-defined
+ * order: lane l (0..63) sums x*x over h in [l*c, l*c+c), c = H/64,
+ * sequential fma from 0; tree64 over the 64 lane sums; mean = fl(sum / H);
+ * inv = fl(1 / fl(sqrt(mean + eps))); then
+ *   out[t,h] = bf16( w[h] * bf16( x[t,h] * inv ) )
+ * (the normalised value is rounded to the activation dtype before the
+ * weight multiply, MLX's rms_norm rounding points). Requires H % 64 == 0. */
+void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out);
+
 /* OLMoE routing: fp32 softmax over E with bf16 probabilities, then the K
  * largest probabilities in descending order, ties to the lower expert id,
  * NaN last; gates are the bf16 probabilities, not renormalised.

@@ -128,6 +128,52 @@ def test_router_logits_one_hot_exact_and_tolerance():
     assert not np.array_equal(oracle.router_logits(xr, w, bias), oracle.router_logits(xr, w))
 
 
+def _rms_f64(x, w, eps):
+    xf, wf = f(x), f(w)
+    return xf / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + eps) * wf
+
+
+def _within_ulps(got, ref, ulps):
+    """|got - ref| <= ulps bf16 ulps of |ref| (ulp of the binade, at least the
+    smallest normal's)."""
+    scale = np.maximum(np.abs(ref), 2.0 ** -126)
+    ulp = 2.0 ** (np.floor(np.log2(scale)) - 7)
+    return np.all(np.abs(got - ref) <= ulps * ulp)
+
+
+@pytest.mark.parametrize("H", [512, 1536, 2048])
+def test_rmsnorm_close_to_float64_and_exact_cases(H):
+    x = bf(RNG.standard_normal((9, H)) * RNG.uniform(0.1, 8.0, (9, 1)))
+    w = bf(RNG.uniform(0.5, 1.5, H))
+    eps = 1e-5
+    got = f(oracle.rmsnorm(x, w, eps))
+    ref = _rms_f64(x, w, eps)
+    # two roundings (the normalised value, then the weighted one)
+    assert _within_ulps(got, ref, 2.0)
+    # constant rows c (a power of two, eps = 0): inv = 1/|c| exactly, so the
+    # output is sign(c) * w bit for bit
+    xc = np.stack([np.full(H, 0.5), np.full(H, -4.0), np.full(H, 2.0 ** -20)]).astype(np.float32)
+    out = oracle.rmsnorm(bf(xc), w, 0.0)
+    np.testing.assert_array_equal(out[0], w)
+    np.testing.assert_array_equal(out[1], w ^ np.uint16(0x8000))
+    np.testing.assert_array_equal(out[2], w)
+    # eps is added to the mean square: a zero row stays zero, a tiny row is
+    # damped by eps
+    z = oracle.rmsnorm(bf(np.zeros((1, H))), w, 1e-5)
+    assert not z.any() or np.all(f(z) == 0.0)
+    tiny = bf(np.full((1, H), 1e-3))
+    assert _within_ulps(f(oracle.rmsnorm(tiny, w, 1e-2)), _rms_f64(tiny, w, 1e-2), 2.0)
+    # planted mistakes fail the same float64 check: no 1/H (sum of squares),
+    # eps dropped on a row where it matters, and a single rounding of x*inv*w
+    # replaced by an unnormalised x * w
+    xf, wf = f(x), f(w)
+    no_mean = xf / np.sqrt((xf ** 2).sum(axis=1, keepdims=True) + eps) * wf
+    assert not _within_ulps(no_mean, ref, 2.0)
+    no_eps = f(tiny) / np.sqrt((f(tiny) ** 2).mean(axis=1, keepdims=True)) * wf
+    assert not _within_ulps(no_eps, _rms_f64(tiny, w, 1e-2), 2.0)
+    assert not _within_ulps(xf * wf, ref, 2.0)
+
+
 def test_olmoe_softmax_close_to_float64():
     lg = bf(RNG.standard_normal((500, 64)) * 2)
     p = f(oracle.olmoe_softmax(lg))

@@ -109,6 +109,9 @@ SIGNATURES = {
     "tfm_moe_forward": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, POINTER(MoeWeights),
                                 c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_size_t,
                                 c_void_p]),
+    "tfm_moe_forward_rmsnorm": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_float,
+                                        POINTER(MoeWeights), c_void_p, c_void_p, c_void_p, c_uint32,
+                                        c_void_p, c_size_t, c_void_p]),
     "tfm_expert_routes_workspace_bytes": (c_size_t, [c_void_p, c_int64]),
     "tfm_expert_routes": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                   POINTER(MoeWeights), c_void_p, c_void_p, c_void_p, c_size_t,

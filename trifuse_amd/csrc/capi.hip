@@ -121,6 +121,7 @@ struct BlockWs {
   int32_t* hist;  // grouping chunk histograms
   int4* slots;    // decode: per active slot {expert, first route, end route, 0}
   float* gates_sorted;  // decode: gates in sorted order
+  uint16_t* xn;         // RMSNorm-ed input [T, H] (tfm_moe_forward_rmsnorm)
   size_t bytes;
 };
 
@@ -144,6 +145,7 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.hist = c.take<int32_t>((size_t)((chunks + 1) * (g.num_experts + 1)));
   w.slots = c.take<int4>((size_t)g.num_experts);
   w.gates_sorted = c.take<float>((size_t)R);
+  w.xn = c.take<uint16_t>((size_t)(T * g.hidden_size));
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -474,6 +476,78 @@ int tfm_moe_experts(const tfm_plan* plan, const void* x, int64_t tokens, const v
   });
 }
 
+// The block on x (already in the layer's dtype and shape): routing, grouping,
+// experts, combine with `residual` (may be null). Inputs are validated by
+// the entry points.
+static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens, const void* residual,
+                             const tfm_moe_weights* weights, void* y, int32_t* idx_out, float* gates_out,
+                             uint32_t flags, BlockWs& ws, hipStream_t s) {
+  const tfm_geometry& g = plan->g;
+  const int64_t R = tokens * g.experts_per_token;
+  const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
+  const int H = g.hidden_size, I = g.intermediate_size;
+  if (fused_decode(g, R)) {
+    {
+      StageScope st(TFM_STAGE_ROUTER, s);
+      launch_decode_route(g.route, static_cast<const uint16_t*>(x),
+                          static_cast<const uint16_t*>(weights->router), weights->logit_bias, T,
+                          H, E, K, ws.logits, ws.idx, ws.gates, s);
+    }
+    // The gate/up kernel publishes the grouping with its slot table and
+    // sorted gates for the down GEMV.
+    Grouping gd = ws.grp;
+    gd.slots = ws.slots;
+    gd.gates_sorted = ws.gates_sorted;
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
+                           weights->gate, weights->up, gd, ws.h, &ws.hdr->status, s);
+    }
+    const int max_active = (int)(R < E ? R : E);
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_gemv_scaled(ws.h, gd, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
+    }
+    {
+      StageScope st(TFM_STAGE_COMBINE, s);
+      launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
+                            static_cast<const uint16_t*>(residual), g.residual_multiplier,
+                            static_cast<uint16_t*>(y), s);
+    }
+    if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
+    if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
+                                   reinterpret_cast<int32_t*>(gates_out), R, s);
+    return;
+  }
+  bool fused_route;
+  {
+    // Router linear, top-k and chunk histograms in one kernel where the
+    // hidden size has a variant; otherwise logits then top-k.
+    StageScope st(TFM_STAGE_ROUTER, s);
+    fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
+                                     static_cast<const uint16_t*>(weights->router),
+                                     weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
+                                     ws.hist, nullptr, s);
+    if (!fused_route)
+      launch_router_logits(static_cast<const uint16_t*>(x),
+                           static_cast<const uint16_t*>(weights->router), weights->logit_bias,
+                           (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+  }
+  if (!fused_route) {
+    StageScope st(TFM_STAGE_TOPK, s);
+    launch_topk_hist(g.route, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
+  }
+  {
+    StageScope st(TFM_STAGE_GROUP, s);
+    launch_group_scatter(ws.idx, R, E, kTopkTokensPerBlock * K, ws.hist, ws.grp, &ws.hdr->status, s);
+  }
+  if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
+  if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
+                                 reinterpret_cast<int32_t*>(gates_out), R, s);
+  run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
+              ws.idx, ws.gates, weights, static_cast<uint16_t*>(y), flags, ws, s, true);
+}
+
 int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const void* residual,
                     const tfm_moe_weights* weights, void* y, int32_t* idx_out, float* gates_out,
                     uint32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
@@ -487,73 +561,39 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
     need_align16(y, "y");
     if (residual) need_align16(residual, "residual");
     check_weights(weights, true);
-    const tfm_geometry& g = plan->g;
-    BlockWs ws = carve_block(g, tokens, workspace);
+    BlockWs ws = carve_block(plan->g, tokens, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    moe_forward_body(plan, x, tokens, residual, weights, y, idx_out, gates_out, flags, ws,
+                     static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_moe_forward_rmsnorm(const tfm_plan* plan, const void* h, int64_t tokens, const void* norm_weight,
+                            float eps, const tfm_moe_weights* weights, void* y, int32_t* idx_out,
+                            float* gates_out, uint32_t flags, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    need(eps >= 0.0f && eps == eps, "eps must be a non-negative number");
+    if (tokens == 0) return;
+    need_ptr(h, "h");
+    need_ptr(norm_weight, "norm_weight");
+    need_ptr(y, "y");
+    need_align16(h, "h");
+    need_align16(norm_weight, "norm_weight");
+    need_align16(y, "y");
+    need(y != h, "y must not alias h (h is the residual)");
+    check_weights(weights, true);
+    BlockWs ws = carve_block(plan->g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t R = tokens * g.experts_per_token;
-    const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
-    const int H = g.hidden_size, I = g.intermediate_size;
-    if (fused_decode(g, R)) {
-      {
-        StageScope st(TFM_STAGE_ROUTER, s);
-        launch_decode_route(g.route, static_cast<const uint16_t*>(x),
-                            static_cast<const uint16_t*>(weights->router), weights->logit_bias, T,
-                            H, E, K, ws.logits, ws.idx, ws.gates, s);
-      }
-      // The gate/up kernel publishes the grouping with its slot table and
-      // sorted gates for the down GEMV.
-      Grouping gd = ws.grp;
-      gd.slots = ws.slots;
-      gd.gates_sorted = ws.gates_sorted;
-      {
-        StageScope st(TFM_STAGE_GATEUP, s);
-        launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
-                             weights->gate, weights->up, gd, ws.h, &ws.hdr->status, s);
-      }
-      const int max_active = (int)(R < E ? R : E);
-      {
-        StageScope st(TFM_STAGE_DOWN, s);
-        launch_gemv_scaled(ws.h, gd, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
-      }
-      {
-        StageScope st(TFM_STAGE_COMBINE, s);
-        launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
-                              static_cast<const uint16_t*>(residual), g.residual_multiplier,
-                              static_cast<uint16_t*>(y), s);
-      }
-      if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
-      if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
-                                     reinterpret_cast<int32_t*>(gates_out), R, s);
-      return;
-    }
-    bool fused_route;
     {
-      // Router linear, top-k and chunk histograms in one kernel where the
-      // hidden size has a variant; otherwise logits then top-k.
-      StageScope st(TFM_STAGE_ROUTER, s);
-      fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
-                                       static_cast<const uint16_t*>(weights->router),
-                                       weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
-                                       ws.hist, nullptr, s);
-      if (!fused_route)
-        launch_router_logits(static_cast<const uint16_t*>(x),
-                             static_cast<const uint16_t*>(weights->router), weights->logit_bias,
-                             (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+      StageScope st(TFM_STAGE_NORM, s);
+      launch_rmsnorm(static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(norm_weight), eps,
+                     (int)tokens, plan->g.hidden_size, ws.xn, s);
     }
-    if (!fused_route) {
-      StageScope st(TFM_STAGE_TOPK, s);
-      launch_topk_hist(g.route, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
-    }
-    {
-      StageScope st(TFM_STAGE_GROUP, s);
-      launch_group_scatter(ws.idx, R, E, kTopkTokensPerBlock * K, ws.hist, ws.grp, &ws.hdr->status, s);
-    }
-    if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
-    if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
-                                   reinterpret_cast<int32_t*>(gates_out), R, s);
-    run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
-                ws.idx, ws.gates, weights, static_cast<uint16_t*>(y), flags, ws, s, true);
+    moe_forward_body(plan, ws.xn, tokens, h, weights, y, idx_out, gates_out, flags, ws, s);
   });
 }
 
@@ -686,7 +726,8 @@ int tfm_profiler_stage(tfm_profiler* p, int32_t stage, double* total_ms, int32_t
 }
 
 const char* tfm_stage_name(int32_t stage) {
-  static const char* names[TFM_STAGE_COUNT] = {"router", "topk", "group", "gateup", "down", "combine"};
+  static const char* names[TFM_STAGE_COUNT] = {"router", "topk", "group", "gateup", "down", "combine",
+                                               "norm"};
   return stage >= 0 && stage < TFM_STAGE_COUNT ? names[stage] : "";
 }
 

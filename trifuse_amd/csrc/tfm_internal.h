@@ -85,6 +85,11 @@ bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, co
 void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
                       float* gates_f32, int32_t* hist, hipStream_t s);
 
+// Post-attention RMSNorm (norm.hip): out = bf16(w * bf16(x * inv)), one wave
+// per row, bit-defined order.
+void launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out,
+                    hipStream_t s);
+
 // Decode path (decode.hip), T*K <= 256 routes.
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,

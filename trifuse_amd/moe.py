@@ -405,6 +405,30 @@ class MoEBlock:
              y.data_ptr(), _ptr(idx), _ptr(gates), flags, ws.data_ptr(), ws.numel(), _stream())
         return (y, idx, gates) if return_routes else y
 
+    def forward_rmsnorm(self, h: torch.Tensor, weights: ExpertWeights, norm_weight: torch.Tensor,
+                        eps: float, return_routes: bool = False):
+        """The block with the post-attention RMSNorm fused in, as the reference
+        layer runs it (MLXNativeGraniteMoEPrefill.h:485-487):
+        post = rms_norm(h, norm_weight, eps); y = h + rm * moe(post).
+        With return_routes, also returns (idx [T,K] int32, gates [T,K] fp32)."""
+        T = self._check_x(h)
+        _dev(norm_weight, "norm_weight")
+        _check_bf16(norm_weight, "norm_weight")
+        if norm_weight.numel() != self.hidden_size or not norm_weight.is_contiguous():
+            raise ValueError("norm_weight must be a contiguous [H] tensor")
+        mw = self._weights(weights, router=True)
+        y = torch.empty_like(h)
+        K = self.experts_per_token
+        idx = gates = None
+        if return_routes:
+            idx = torch.empty((T, K), dtype=torch.int32, device=h.device)
+            gates = torch.empty((T, K), dtype=torch.float32, device=h.device)
+        ws = self.workspace(T, h.device)
+        call("tfm_moe_forward_rmsnorm", self._plan, h.data_ptr(), T, norm_weight.data_ptr(), float(eps),
+             ctypes.byref(mw), y.data_ptr(), _ptr(idx), _ptr(gates), 0, ws.data_ptr(), ws.numel(),
+             _stream())
+        return (y, idx, gates) if return_routes else y
+
     def route(self, x: torch.Tensor, router: torch.Tensor, logit_bias: Optional[torch.Tensor] = None):
         """Router linear + routing: (idx [T,K] int32, gates [T,K], logits [T,E] bf16).
         OLMoE gates are bf16 probabilities; Granite gates are fp32."""
@@ -467,7 +491,7 @@ class MoEBlock:
 class StageProfiler:
     """HIP-event timing of the library's kernel stages (tfm_profiler_*)."""
 
-    STAGES = ("router", "topk", "group", "gateup", "down", "combine")
+    STAGES = ("router", "topk", "group", "gateup", "down", "combine", "norm")
 
     def __init__(self, capacity: int = 4096):
         self._lib = _lib.load()
