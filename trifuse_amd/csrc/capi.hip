@@ -122,6 +122,7 @@ struct BlockWs {
   int4* slots;    // decode: per active slot {expert, first route, end route, 0}
   float* gates_sorted;  // decode: gates in sorted order
   uint16_t* xn;         // RMSNorm-ed input [T, H] (tfm_moe_forward_rmsnorm)
+  int32_t* meta;        // decode: [0] = active slot count
   size_t bytes;
 };
 
@@ -146,6 +147,7 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.slots = c.take<int4>((size_t)g.num_experts);
   w.gates_sorted = c.take<float>((size_t)R);
   w.xn = c.take<uint16_t>((size_t)(T * g.hidden_size));
+  w.meta = c.take<int32_t>(64);
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -225,6 +227,30 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
   const int64_t R = T * K;
   const bool gemv = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
+  if (!grouped && gemv && decode_stream_fits((int)T, K, E, H, I)) {
+    // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
+    // shapes, so both entry points give bit-identical results.
+    Grouping gd = ws.grp;
+    gd.slots = ws.slots;
+    gd.gates_sorted = ws.gates_sorted;
+    {
+      StageScope st(TFM_STAGE_GROUP, s);
+      launch_ds_group_given(idx, gates, (int)T, E, K, gd, ws.meta, &ws.hdr->status, s);
+    }
+    const int max_active = (int)(R < E ? R : E);
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ds_gateup(x, (int)T, K, H, I, max_active, w->gate, w->up, gd, ws.meta, ws.h, s);
+    }
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_ds_down(ws.h, H, I, max_active, w->down, gd, ws.meta, ws.P, s);
+    }
+    StageScope st(TFM_STAGE_COMBINE, s);
+    launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
+                          g.residual_multiplier, y, s);
+    return;
+  }
   if (!grouped) {
     StageScope st(TFM_STAGE_GROUP, s);
     launch_group(idx, R, E, ws.grp, ws.hist, &ws.hdr->status, s);
@@ -486,6 +512,41 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const int64_t R = tokens * g.experts_per_token;
   const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
   const int H = g.hidden_size, I = g.intermediate_size;
+  if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I)) {
+    Grouping gd = ws.grp;
+    gd.slots = ws.slots;
+    gd.gates_sorted = ws.gates_sorted;
+    {
+      StageScope st(TFM_STAGE_ROUTER, s);
+      launch_decode_logits(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(weights->router),
+                           weights->logit_bias, T, H, E, ws.logits, s);
+    }
+    {
+      StageScope st(TFM_STAGE_TOPK, s);
+      launch_ds_topk_group(g.route, ws.logits, T, E, K, ws.idx, ws.gates, gd, ws.meta,
+                           &ws.hdr->status, s);
+    }
+    const int max_active = (int)(R < E ? R : E);
+    {
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ds_gateup(static_cast<const uint16_t*>(x), T, K, H, I, max_active, weights->gate,
+                       weights->up, gd, ws.meta, ws.h, s);
+    }
+    {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_ds_down(ws.h, H, I, max_active, weights->down, gd, ws.meta, ws.P, s);
+    }
+    {
+      StageScope st(TFM_STAGE_COMBINE, s);
+      launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
+                            static_cast<const uint16_t*>(residual), g.residual_multiplier,
+                            static_cast<uint16_t*>(y), s);
+    }
+    if (idx_out) launch_copy_i32(ws.idx, idx_out, R, s);
+    if (gates_out) launch_copy_i32(reinterpret_cast<const int32_t*>(ws.gates),
+                                   reinterpret_cast<int32_t*>(gates_out), R, s);
+    return;
+  }
   if (fused_decode(g, R)) {
     {
       StageScope st(TFM_STAGE_ROUTER, s);

@@ -227,6 +227,21 @@ static int lg_for(int kin) {
   return nch <= 4 ? 4 : nch <= 8 ? 8 : nch <= 16 ? 16 : nch <= 32 ? 32 : 64;
 }
 
+void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
+                          int E, uint16_t* logits, hipStream_t s) {
+  if (T <= 0) return;
+  if (E > 64) fail(TFM_E_UNSUPPORTED, "decode routing: more than 64 experts");
+  if (!logits) fail(TFM_E_INVALID, "decode routing: logits buffer missing");
+  switch (H) {
+    case 512: decode_logits_kernel<8><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1024: decode_logits_kernel<16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1536: decode_logits_kernel<24><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 2048: decode_logits_kernel<32><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    default: decode_logits_generic<<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+  }
+  check_hip(hipGetLastError(), "decode logits launch");
+}
+
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s) {

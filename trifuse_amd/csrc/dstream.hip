@@ -1,0 +1,757 @@
+// Decode path, streaming form (few routes: T*K <= 256, small T).
+//
+// The block NativeGraniteMoEPrefill::moe runs per layer
+// (MLXNativeGraniteMoEPrefill.h:627-702) at decode shapes, as five kernels:
+//   1. decode_logits_kernel (decode.hip): router logits, one workgroup per expert,
+//   2. ds_topk_group_kernel: one workgroup ranks every token (OLMoE or Granite
+//      rules, route_wave.h) and groups the T*K routes by expert (stable), then
+//      publishes the grouping, a slot table {expert, first route, end route}
+//      and the active-slot count,
+//   3. ds_gateup_kernel: dequant GEMV of gate and up with the SwiGLU epilogue,
+//   4. ds_down_kernel: dequant GEMV of down, scaled by each route's gate (fp32),
+//   5. combine_sorted_kernel (combine.hip): ordered K reduction + residual.
+//
+// Work split of the two GEMV kernels. An item is a few rows of one routed
+// expert (4 rows per wave-wide load: 16 lanes per row, each lane owning
+// 32-element chunks 16c + l of the row, one 16-byte load per chunk). Items
+// are ordered (active slot, row block) and every wave takes a contiguous range
+// of them, cut by cost (a fixed share for the nibble unpack plus one share per
+// route of the expert), so hot experts do not leave a tail. A wave loads its
+// range's slot data once, issues the loads of its next item before it reduces
+// and stores the current one, and never waits on another wave after the
+// start: gate/up stages the x rows of all T tokens once per workgroup; down
+// stages the h rows of the current expert's routes per wave.
+//
+// Arithmetic per chunk (inside one 64-wide group) as in the other GEMVs:
+//   sum_k x_k (s q_k + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k,
+// with (128 + q) built exactly in bf16 by byte permutes and the products run
+// as v_dot2_f32_bf16 with fp32 accumulation (no MFMA).
+#include <algorithm>
+#include <cstdlib>
+
+#include "gemv_body.h"
+#include "route_wave.h"
+
+namespace tfm {
+
+constexpr int kDsCostUnpack = 2;  // item cost = kDsCostUnpack + routes of its expert
+constexpr int kDsDownXB = 4;      // h rows staged per wave in the down kernel
+
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+// Marks a wave-uniform value as such, so that buffer resources built from it
+// stay in scalar registers.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Slot data of the active experts (one slot per lane; the slot table also
+// carries the active count in .w) and the contiguous range [i0, i1) of flat
+// item indices i = slot * ipe + row block of wave `gw` of `nw` waves. The
+// range is cut by cost, item cost = kDsCostUnpack + routes of its slot: the
+// wave takes the items whose start cost lies in [gw, gw+1) * total / nw.
+struct WaveRange {
+  int4 sl;     // this lane's slot {expert, first route, end route, active count}
+  int ipe;     // items (row blocks) per expert
+  int i0, i1;  // flat item range
+};
+
+__device__ __forceinline__ int4 load_slot(const int4* __restrict__ slots, int E) {
+  const int lane = threadIdx.x & 63;
+  return lane < E ? slots[lane] : make_int4(-1, 0, 0, 0);
+}
+
+// sl: load_slot's result (lane 0's slot always exists, E >= 1).
+__device__ __forceinline__ void wave_range(int4 sl, int ipe, int gw, int nw, WaveRange& w) {
+  const int lane = threadIdx.x & 63;
+  w.ipe = ipe;
+  w.sl = sl;
+  const int U = uni(w.sl.w);
+  const bool on = lane < U;
+  const int rl = on ? w.sl.z - w.sl.y : 0;
+  const int cost = on ? ipe * (kDsCostUnpack + rl) : 0;
+  const int incl = wave_incl_scan(cost);
+  const int total = readlane_i(incl, 63);
+  const int c0 = (int)((int64_t)gw * total / nw);
+  const int c1 = (int)((int64_t)(gw + 1) * total / nw);
+  // First item whose start cost is >= c: its slot is the count of slots whose
+  // inclusive cost is <= c; within the slot, start cost = excl + r * weight.
+  auto first = [&](int c) -> int {
+    const int a = __popcll(__ballot(on && incl <= c));
+    if (a >= U) return U * ipe;
+    const int excl = readlane_i(incl - cost, a);
+    const int wgt = kDsCostUnpack + readlane_i(rl, a);
+    const int rr = (c - excl + wgt - 1) / wgt;
+    return rr >= ipe ? (a + 1) * ipe : a * ipe + rr;
+  };
+  w.i0 = uni(first(c0));
+  w.i1 = uni(first(c1));
+}
+
+// ---------------------------------------------------------------------------
+// 2. Top-k of every token and the stable grouping of the T*K routes.
+// One workgroup of 16 waves; wave w ranks tokens w, w+16, ...; the first four
+// waves then group (one thread per route). MODE kDsGiven takes the routes
+// (ids and fp32 gates) from idx/gates instead of ranking: ids outside [0, E)
+// sort after every valid id (bucket E), are left out of the slot table and
+// set TFM_STATUS_BAD_EXPERT_ID.
+constexpr int kDsGiven = 2;
+
+template <int MODE>
+__device__ __forceinline__ void ds_rank_group(const uint16_t* __restrict__ logits, int T, int E, int K,
+                                              int32_t* __restrict__ idx, float* __restrict__ gates,
+                                              const Grouping& g, int32_t* __restrict__ meta,
+                                              uint32_t* __restrict__ status) {
+  __shared__ int s_e[256];
+  __shared__ float s_g[256];
+  __shared__ int wcnt[4][65];
+  __shared__ int wpre[4][65];
+  __shared__ int s_off[66];
+  __shared__ int s_act[65];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int R = T * K;
+  if (MODE == kDsGiven) {
+    if (tid < R) {
+      const int id = idx[tid];
+      s_e[tid] = (id < 0 || id >= E) ? E : id;
+      s_g[tid] = gates[tid];
+    }
+  } else {
+    for (int t = wave; t < T; t += 16) {
+      const uint16_t* row = logits + (int64_t)t * E;
+      float gv;
+      int id;
+      if (MODE == TFM_ROUTE_OLMOE) {
+        uint16_t gb;
+        id = olmoe_route_wave(row, E, K, &gv, &gb);
+      } else {
+        id = granite_route_wave(row, E, K, &gv);
+      }
+      if (lane < K) {
+        s_e[t * K + lane] = id;
+        s_g[t * K + lane] = gv;
+        idx[(int64_t)t * K + lane] = id;
+        gates[(int64_t)t * K + lane] = gv;
+      }
+    }
+  }
+  if (tid < 4 * 65) (&wcnt[0][0])[tid] = 0;
+  __syncthreads();
+  // Stable grouping: position of route f = routes to lower buckets + routes
+  // to its bucket with a lower flat index (buckets 0..E, E = bad ids).
+  const bool live = tid < R;
+  const int e = live ? s_e[tid] : 0;
+  int rank_w = 0;
+  if (wave < 4) {
+    uint64_t match = __ballot(live);
+#pragma unroll
+    for (int bit = 0; bit < 7; ++bit) {
+      const bool b = (e >> bit) & 1;
+      const uint64_t ones = __ballot(live && b);
+      match &= b ? ones : ~ones;
+    }
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    rank_w = __popcll(match & lt);
+    if (live && rank_w == 0) wcnt[wave][e] = __popcll(match);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // Lanes 0..63 hold experts 0..63; the bad bucket E (<= 64) comes last.
+    const int c0 = wcnt[0][lane], c1 = wcnt[1][lane], c2 = wcnt[2][lane], c3 = wcnt[3][lane];
+    const int cnt = lane < E ? c0 + c1 + c2 + c3 : 0;
+    const int incl = wave_incl_scan(cnt);
+    const int excl = incl - cnt;
+    if (lane < E) {
+      s_off[lane] = excl;
+      wpre[0][lane] = excl;
+      wpre[1][lane] = excl + c0;
+      wpre[2][lane] = excl + c0 + c1;
+      wpre[3][lane] = excl + c0 + c1 + c2;
+    }
+    if (lane == 63) {
+      s_off[E] = incl;
+      int b = incl;
+      wpre[0][E] = b; b += wcnt[0][E];
+      wpre[1][E] = b; b += wcnt[1][E];
+      wpre[2][E] = b; b += wcnt[2][E];
+      wpre[3][E] = b;
+      s_off[E + 1] = b + wcnt[3][E];  // == R
+    }
+    const uint64_t act = __ballot(lane < E && cnt > 0);
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if (lane < E && cnt > 0) s_act[__popcll(act & lt)] = lane;
+    if (lane == 0) s_act[E] = __popcll(act);
+  }
+  __syncthreads();
+  if (live) {
+    const int pos = wpre[wave][e] + rank_w;
+    g.order[pos] = tid;
+    g.inverse[tid] = pos;
+    g.gates_sorted[pos] = s_g[tid];
+  }
+  const int U = s_act[E];
+  if (tid <= E) {
+    g.offsets[tid] = s_off[tid];
+    if (tid == E || tid < U) g.active[tid] = s_act[tid];
+  }
+  if (tid < E) {
+    const int ex = tid < U ? s_act[tid] : -1;
+    g.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, U) : make_int4(ex, s_off[ex], s_off[ex + 1], U);
+  }
+  if (tid == 0) {
+    meta[0] = U;
+    *status = s_off[E] < R ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(1024) void ds_topk_group_kernel(const uint16_t* __restrict__ logits,
+                                                             int T, int E, int K,
+                                                             int32_t* __restrict__ idx,
+                                                             float* __restrict__ gates,
+                                                             Grouping g, int32_t* __restrict__ meta,
+                                                             uint32_t* __restrict__ status) {
+  ds_rank_group<MODE>(logits, T, E, K, idx, gates, g, meta, status);
+}
+
+// ---------------------------------------------------------------------------
+// Raw loads of one chunk of one row: 16 packed bytes and its group's scale and
+// bias (bf16 in the low half).
+struct DsRaw {
+  uint4 q;
+  uint32_t s, b;
+};
+
+struct DsMat {
+  __amdgpu_buffer_rsrc_t q, s, b;
+};
+
+// Buffer resources over expert e's rows of one matrix; rows >= N read zero.
+__device__ __forceinline__ DsMat ds_mat(const tfm_affine& m, int e, int N, int kin) {
+  const uint32_t qrow = (uint32_t)kin / 2, srow = (uint32_t)kin / 32;
+  DsMat d;
+  d.q = make_rsrc(reinterpret_cast<const char*>(m.q) + (size_t)e * N * qrow, (uint32_t)N * qrow);
+  d.s = make_rsrc(static_cast<const char*>(m.scales) + (size_t)e * N * srow, (uint32_t)N * srow);
+  d.b = make_rsrc(static_cast<const char*>(m.biases) + (size_t)e * N * srow, (uint32_t)N * srow);
+  return d;
+}
+
+// Chunk c (c < C) of row n for lane column ll: element offset 32 * (16c + ll).
+template <int C>
+__device__ __forceinline__ void ds_load_row(const DsMat& m, int n, int kin, int ll, DsRaw (&w)[C]) {
+  const uint32_t qrow = (uint32_t)kin / 2, srow = (uint32_t)kin / 32;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const uint32_t k = 16u * c + ll;
+    const uint32_t qo = (uint32_t)n * qrow + 16u * k;
+    const uint32_t so = (uint32_t)n * srow + 2u * (k >> 1);
+    w[c].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.q, qo, 0, 0));
+    w[c].s = __builtin_amdgcn_raw_buffer_load_b16(m.s, so, 0, 0);
+    w[c].b = __builtin_amdgcn_raw_buffer_load_b16(m.b, so, 0, 0);
+  }
+}
+
+constexpr int kDsXChunks = 4;  // most x chunks staged per thread by the gate/up prologue
+
+// Store one raw 32-element x chunk (4 x 16 bytes) in dot2 pair order:
+// xs[(slot*4 + q)*nch + k], and its sum in xsum[slot*nch + k].
+__device__ __forceinline__ void ds_store_chunk(const uint4 (&r)[4], uint4* xs, float* xsum, int slot, int k,
+                                               int nch) {
+  const uint32_t ones = 0x3f803f80u;  // (1.0, 1.0) in bf16
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 v = r[i];
+    xs[(slot * 4 + i) * nch + k] = make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u),
+                                              __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                                              __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                                              __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+    sum = dot2(v.x, ones, sum);
+    sum = dot2(v.y, ones, sum);
+    sum = dot2(v.z, ones, sum);
+    sum = dot2(v.w, ones, sum);
+  }
+  xsum[slot * nch + k] = sum;
+}
+
+// Stage one 32-element x chunk in pair order: xs[(slot*4 + q)*nch + k], xsum[slot*nch + k].
+__device__ __forceinline__ void ds_stage_chunk(const uint16_t* __restrict__ src, uint4* xs, float* xsum,
+                                               int slot, int k, int nch) {
+  ChunkX cx;
+  load_x(src, cx);
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    xs[(slot * 4 + q) * nch + k] = make_uint4(cx.p[4 * q], cx.p[4 * q + 1], cx.p[4 * q + 2], cx.p[4 * q + 3]);
+  xsum[slot * nch + k] = cx.sum;
+}
+
+// ---------------------------------------------------------------------------
+// 3. gate/up GEMV + SwiGLU: h[j, n] = bf16(silu(x_t . gate_n) * (x_t . up_n)),
+// t = order[j] / K, for sorted routes j. Item = 4 rows of gate and of up. Two
+// items are in flight per wave: the loads of item i+2 go out as soon as the
+// dot products of item i have consumed its registers.
+struct DsGateUpArgs {
+  const uint16_t* x;  // [T, H]
+  int T, K, E, H, I;
+  tfm_affine gate, up;
+  const int4* slots;  // [E] {expert, first route, end route, active count}
+  const int32_t* order;
+  uint16_t* h;  // [R, I]
+};
+
+template <int C>
+struct DsGU {
+  DsRaw g[C], u[C];
+};
+
+// Dot products of one gate/up item with one staged token row:
+// ag/au = sum over the lane's chunks of s*sum(x(128+q)) + (b-128s)*sum(x).
+// The four LDS reads of a chunk go out together, ahead of its dot products.
+template <int C>
+__device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restrict__ xs,
+                                          const float* __restrict__ xsum, int tok, int ll, float& ag,
+                                          float& au) {
+  constexpr int nch = 16 * C;
+  ag = au = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int k = 16 * c + ll;
+    uint4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = xs[(tok * 4 + q) * nch + k];
+    const float xsm = xsum[tok * nch + k];
+    const float sg = bf2f((uint16_t)w.g[c].s), su = bf2f((uint16_t)w.u[c].s);
+    const float cg = __builtin_fmaf(-128.0f, sg, bf2f((uint16_t)w.g[c].b));
+    const float cu = __builtin_fmaf(-128.0f, su, bf2f((uint16_t)w.u[c].b));
+    float dg = 0.0f, du = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // Opaque copies keep the unpack inside the route loop: hoisted out of
+      // it, the unpacked item would need 128 more registers.
+      uint32_t wg = word_of(w.g[c].q, q), wu = word_of(w.u[c].q, q);
+      asm volatile("" : "+v"(wg), "+v"(wu));
+      uint32_t pg[4], pu[4];
+      unpack_word(wg, pg);
+      unpack_word(wu, pu);
+      dg = dot2(pg[0], v[q].x, dg);
+      du = dot2(pu[0], v[q].x, du);
+      dg = dot2(pg[1], v[q].y, dg);
+      du = dot2(pu[1], v[q].y, du);
+      dg = dot2(pg[2], v[q].z, dg);
+      du = dot2(pu[2], v[q].z, du);
+      dg = dot2(pg[3], v[q].w, dg);
+      du = dot2(pu[3], v[q].w, du);
+    }
+    ag += __builtin_fmaf(sg, dg, cg * xsm);
+    au += __builtin_fmaf(su, du, cu * xsm);
+  }
+}
+
+template <int C, int XCH, int NT, int PIPE>
+__global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
+  extern __shared__ uint4 ds_lds[];
+  const int H = A.H, N = A.I, T = A.T, K = A.K;
+  const int R = T * K;
+  constexpr int nch = 16 * C;
+  uint4* xs = ds_lds;                                        // [T][4][nch]
+  float* xsum = reinterpret_cast<float*>(xs + T * 4 * nch);  // [T][nch]
+  int* s_tok = reinterpret_cast<int*>(xsum + T * nch);       // [R]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int ll = lane & 15, rsub = lane >> 4;
+  const int gw = blockIdx.x * (NT / 64) + (tid >> 6), nw = gridDim.x * (NT / 64);
+
+  // Prologue, ordered so that its memory latencies overlap: the slot table,
+  // the x rows of every token (at most XCH 32-element chunks per thread) and
+  // the route tokens are requested first; the first two items'
+  // weights as soon as the slot table is in; the x rows are permuted into
+  // dot2 pair order and stored while those weights are in flight.
+  const int4 sl = load_slot(A.slots, A.E);
+  uint4 xr[XCH][4];
+#pragma unroll
+  for (int u = 0; u < XCH; ++u) {
+    const int p = tid + NT * u;
+    if (p < T * nch) {
+      const uint4* src = reinterpret_cast<const uint4*>(A.x + (int64_t)(p / nch) * H + 32 * (p % nch));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) xr[u][v] = src[v];
+    }
+  }
+  const int otok = tid < R ? A.order[tid] : 0;
+  WaveRange wr;
+  const int ipe = (N + 3) / 4;
+  wave_range(sl, ipe, gw, nw, wr);
+  auto load = [&](DsGU<C>& w, int i) {
+    const int a = i / ipe;
+    const int e = uni(readlane_i(wr.sl.x, a));
+    const int n = (i - a * ipe) * 4 + rsub;
+    ds_load_row<C>(ds_mat(A.gate, e, N, H), n, H, ll, w.g);
+    ds_load_row<C>(ds_mat(A.up, e, N, H), n, H, ll, w.u);
+  };
+  DsGU<C> wA, wB;
+  if (wr.i0 < wr.i1) load(wA, wr.i0);
+  if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
+  if (tid < R) s_tok[tid] = otok / K;
+#pragma unroll
+  for (int u = 0; u < XCH; ++u) {
+    const int p = tid + NT * u;
+    if (p < T * nch) ds_store_chunk(xr[u], xs, xsum, p / nch, p % nch, nch);
+  }
+  __syncthreads();
+
+  auto emit = [&](int j, int n, float ag, float au) {
+    const float gt = dpp_group_sum<16>(ag);
+    const float up = dpp_group_sum<16>(au);
+    if (ll == 0 && n < N) {
+      const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
+      A.h[(int64_t)j * N + n] = f2bf(hv);
+    }
+  };
+  // Routes one at a time through one branch-free body (the nibble unpack is
+  // redone per route: at decode most experts have one or two routes). PIPE
+  // items are in flight per wave: when every route of item i is done, its
+  // registers are refilled with item i + PIPE.
+  auto step = [&](DsGU<C>& w, int i) {
+    const int a = i / ipe;
+    const int n = (i - a * ipe) * 4 + rsub;
+    const int j0 = uni(readlane_i(wr.sl.y, a)), j1 = uni(readlane_i(wr.sl.z, a));
+    for (int j = j0; j < j1; ++j) {
+      float ag, au;
+      ds_gu_dot<C>(w, xs, xsum, s_tok[j], ll, ag, au);
+      emit(j, n, ag, au);
+    }
+    if (i + PIPE < wr.i1) load(w, i + PIPE);
+  };
+  if (PIPE == 1) {
+    for (int i = wr.i0; i < wr.i1; ++i) step(wA, i);
+  } else {
+    for (int i = wr.i0; i < wr.i1; i += 2) {
+      step(wA, i);
+      if (i + 1 < wr.i1) step(wB, i + 1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. down GEMV scaled by the gate: P[j, n] = gate_j * (h_j . down_n) (fp32),
+// sorted routes j. Item = 4*RG rows; two items in flight per wave. Each wave
+// stages the h rows of up to kDsDownXB routes of its current expert in its
+// own LDS region.
+struct DsDownArgs {
+  const uint16_t* h;  // [R, I] sorted rows
+  int E, H, I;
+  tfm_affine down;
+  const int4* slots;
+  const float* gates_sorted;
+  float* P;  // [R, H]
+};
+
+template <int C, int RG>
+struct DsDn {
+  DsRaw r[RG][C];
+};
+
+// Dot products of one down item with staged h row t.
+template <int C, int RG>
+__device__ __forceinline__ void ds_dn_dot(const DsDn<C, RG>& w, const uint4* __restrict__ xs,
+                                          const float* __restrict__ xsum, int t, int ll,
+                                          float (&acc)[RG]) {
+  constexpr int nch = 16 * C;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) acc[g] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int k = 16 * c + ll;
+    uint4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = xs[(t * 4 + q) * nch + k];
+    const float xsm = xsum[t * nch + k];
+    float d[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) d[g] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        uint32_t wq = word_of(w.r[g][c].q, q);
+        asm volatile("" : "+v"(wq));  // keeps the unpack inside the route loop
+        uint32_t p[4];
+        unpack_word(wq, p);
+        d[g] = dot2(p[0], v[q].x, d[g]);
+        d[g] = dot2(p[1], v[q].y, d[g]);
+        d[g] = dot2(p[2], v[q].z, d[g]);
+        d[g] = dot2(p[3], v[q].w, d[g]);
+      }
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const float sc = bf2f((uint16_t)w.r[g][c].s);
+      const float cc = __builtin_fmaf(-128.0f, sc, bf2f((uint16_t)w.r[g][c].b));
+      acc[g] += __builtin_fmaf(sc, d[g], cc * xsm);
+    }
+  }
+}
+
+template <int C, int RG, int NT, int PIPE>
+__global__ __launch_bounds__(NT) void ds_down_kernel(DsDownArgs A) {
+  extern __shared__ uint4 ds_lds[];
+  constexpr int XB = kDsDownXB;
+  constexpr int nch = 16 * C;
+  const int N = A.H, kin = A.I;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int ll = lane & 15, rsub = lane >> 4;
+  const int gw = blockIdx.x * (NT / 64) + wave, nw = gridDim.x * (NT / 64);
+  constexpr int region = XB * 4 * nch + (XB * nch + 3) / 4;  // uint4 per wave
+  uint4* xs = ds_lds + wave * region;
+  float* xsum = reinterpret_cast<float*>(xs + XB * 4 * nch);
+
+  WaveRange wr;
+  const int ipe = (N + 4 * RG - 1) / (4 * RG);
+  wave_range(load_slot(A.slots, A.E), ipe, gw, nw, wr);
+  auto load = [&](DsDn<C, RG>& w, int i) {
+    const int a = i / ipe;
+    const int e = uni(readlane_i(wr.sl.x, a));
+    const int r = i - a * ipe;
+    const DsMat m = ds_mat(A.down, e, N, kin);
+#pragma unroll
+    for (int g = 0; g < RG; ++g) ds_load_row<C>(m, r * 4 * RG + 4 * g + rsub, kin, ll, w.r[g]);
+  };
+  DsDn<C, RG> wA, wB;
+  if (wr.i0 < wr.i1) load(wA, wr.i0);
+  if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
+  int staged_j = -1;  // first route of the staged batch
+  float gv = 0.0f;    // lane t: gate of staged route t
+
+  auto stage = [&](int jb, int nb) {
+    if (staged_j == jb) return;
+    // The previous batch's reads of this region come first in program
+    // order, and LDS operations of one wave complete in order.
+    for (int p = lane; p < nb * nch; p += 64) {
+      const int t = p / nch, k = p % nch;
+      ds_stage_chunk(A.h + (int64_t)(jb + t) * kin + 32 * k, xs, xsum, t, k, nch);
+    }
+    gv = lane < nb ? A.gates_sorted[jb + lane] : 0.0f;
+    staged_j = jb;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto emit = [&](int j, int t, int r, const float (&acc)[RG]) {
+    const float gt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), t));
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const float sum = dpp_group_sum<16>(acc[g]);
+      const int n = r * 4 * RG + 4 * g + rsub;
+      if (ll == 0 && n < N) A.P[(int64_t)j * N + n] = sum * gt;
+    }
+  };
+  auto step = [&](DsDn<C, RG>& w, int i) {
+    const int a = i / ipe;
+    const int r = i - a * ipe;
+    const int j0 = uni(readlane_i(wr.sl.y, a)), j1 = uni(readlane_i(wr.sl.z, a));
+    for (int jb = j0; jb < j1; jb += XB) {
+      const int nb = min(XB, j1 - jb);
+      stage(jb, nb);
+      for (int t = 0; t < nb; ++t) {
+        float acc[RG];
+        ds_dn_dot<C, RG>(w, xs, xsum, t, ll, acc);
+        emit(jb + t, t, r, acc);
+      }
+    }
+    if (i + PIPE < wr.i1) load(w, i + PIPE);
+  };
+  if (PIPE == 1) {
+    for (int i = wr.i0; i < wr.i1; ++i) step(wA, i);
+  } else {
+    for (int i = wr.i0; i < wr.i1; i += 2) {
+      step(wA, i);
+      if (i + 1 < wr.i1) step(wB, i + 1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+static int device_cus() {
+  static int cus = [] {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    return n;
+  }();
+  return cus;
+}
+
+static int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* s = std::getenv(name);
+  if (!s) return dflt;
+  char* end = nullptr;
+  const long v = std::strtol(s, &end, 10);
+  if (!end || *end != 0 || v < lo || v > hi) return dflt;
+  return (int)v;
+}
+
+static size_t ds_gateup_lds(int T, int K, int H) {
+  const int nch = H / 32;
+  return (size_t)T * nch * 4 * 16 + (size_t)T * nch * 4 + (size_t)T * K * 4;
+}
+
+static size_t ds_down_lds(int I, int threads) {
+  const int nch = I / 32;
+  return (size_t)(threads / 64) * ((size_t)kDsDownXB * 4 * nch * 16 + (((size_t)kDsDownXB * nch + 3) / 4) * 16);
+}
+
+bool decode_stream_fits(int T, int K, int E, int H, int I) {
+  const bool w_ok = (H % 512 == 0) && H >= 512 && H <= 2048 && (I % 512 == 0) && I >= 512 && I <= 2048;
+  return w_ok && E <= 64 && T * K <= 256 && T >= 1 && T * (H / 32) <= 256 * kDsXChunks &&
+         ds_gateup_lds(T, K, H) <= 64 * 1024 &&
+         ds_down_lds(I, 256) <= 64 * 1024;
+}
+
+void launch_ds_topk_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                          float* gates, const Grouping& g, int32_t* meta, uint32_t* status,
+                          hipStream_t s) {
+  if (T * K > 256 || E > 64) fail(TFM_E_INVALID, "decode top-k/grouping: more than 256 routes or 64 experts");
+  if (route_kind == TFM_ROUTE_OLMOE)
+    ds_topk_group_kernel<TFM_ROUTE_OLMOE><<<1, 1024, 0, s>>>(logits, T, E, K, idx, gates, g, meta, status);
+  else
+    ds_topk_group_kernel<TFM_ROUTE_GRANITE><<<1, 1024, 0, s>>>(logits, T, E, K, idx, gates, g, meta, status);
+  check_hip(hipGetLastError(), "decode top-k/grouping launch");
+}
+
+void launch_ds_group_given(const int32_t* idx, const float* gates, int T, int E, int K, const Grouping& g,
+                           int32_t* meta, uint32_t* status, hipStream_t s) {
+  if (T * K > 256 || E > 64) fail(TFM_E_INVALID, "decode grouping: more than 256 routes or 64 experts");
+  ds_topk_group_kernel<kDsGiven><<<1, 1024, 0, s>>>(nullptr, T, E, K, const_cast<int32_t*>(idx),
+                                                   const_cast<float*>(gates), g, meta, status);
+  check_hip(hipGetLastError(), "decode grouping launch");
+}
+
+// Workgroups resident per compute unit for a kernel at a block and dynamic
+// LDS size (cached per kernel and size; the first query goes to the runtime).
+template <typename Kern>
+static int resident_per_cu(Kern kern, int threads, size_t lds) {
+  struct Entry {
+    const void* k;
+    size_t lds;
+    int n;
+  };
+  static thread_local Entry cache[32];
+  static thread_local int used = 0;
+  const void* key = reinterpret_cast<const void*>(kern);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == key && cache[i].lds == lds) return cache[i].n;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess || n <= 0) n = 1;
+  if (used < 32) cache[used++] = Entry{key, lds, n};
+  return n;
+}
+
+// One resident round of workgroups (every wave then streams a contiguous
+// item range), capped so that every wave has at least one item.
+template <typename Kern>
+static unsigned ds_grid(Kern kern, int threads, size_t lds, int64_t max_items) {
+  const int per_cu = env_int("TFM_DS_WG_PER_CU", resident_per_cu(kern, threads, lds), 1, 16);
+  const int64_t cap = (int64_t)device_cus() * per_cu;
+  const int64_t want = (max_items + threads / 64 - 1) / (threads / 64);
+  return (unsigned)std::max<int64_t>(1, std::min(cap, want));
+}
+
+// Raises a kernel's dynamic LDS limit (64 KiB by default) once per kernel.
+template <typename Kern>
+static void allow_lds(Kern kern, size_t lds) {
+  if (lds <= 64 * 1024) return;
+  static thread_local const void* done[16];
+  static thread_local int used = 0;
+  const void* key = reinterpret_cast<const void*>(kern);
+  for (int i = 0; i < used; ++i)
+    if (done[i] == key) return;
+  check_hip(hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+            "decode down: LDS limit");
+  if (used < 16) done[used++] = key;
+}
+
+// Threads per workgroup of the streaming GEMVs: 256 measured faster than
+// 1024 (one workgroup per compute unit) at decode shapes.
+static int ds_threads() { return env_int("TFM_DS_THREADS", 256, 256, 1024) >= 1024 ? 1024 : 256; }
+
+void launch_ds_gateup(const uint16_t* x, int T, int K, int H, int I, int max_active,
+                      const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
+                      const int32_t* meta, uint16_t* h, hipStream_t s) {
+  (void)meta;
+  DsGateUpArgs A{};
+  A.x = x; A.T = T; A.K = K; A.E = g.E; A.H = H; A.I = I; A.gate = gate; A.up = up;
+  A.slots = g.slots; A.order = g.order; A.h = h;
+  const size_t lds = ds_gateup_lds(T, K, H);
+  const int64_t items = (int64_t)max_active * ((I + 3) / 4);
+  const int nt = ds_threads();
+  const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
+  const int per = T * (H / 32);
+  const int xch = per <= nt ? 1 : per <= 2 * nt ? 2 : 4;
+#define TFM_DS_GU_P(CV, XV, NV, PV) \
+  ds_gateup_kernel<CV, XV, NV, PV><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV>, NV, lds, items), NV, lds, s>>>(A);
+#define TFM_DS_GU_X(CV, XV, NV) \
+  if (pipe == 2 && NV == 256) { TFM_DS_GU_P(CV, XV, 256, 2) } else { TFM_DS_GU_P(CV, XV, NV, 1) }
+#define TFM_DS_GU(CV)                                           \
+  if (nt == 1024) {                                             \
+    if (xch == 1) TFM_DS_GU_X(CV, 1, 1024) else TFM_DS_GU_X(CV, 2, 1024) \
+  } else if (xch == 1) TFM_DS_GU_X(CV, 1, 256)                  \
+  else if (xch == 2) TFM_DS_GU_X(CV, 2, 256)                    \
+  else TFM_DS_GU_X(CV, 4, 256)
+  switch (H / 512) {
+    case 1: TFM_DS_GU(1) break;
+    case 2: TFM_DS_GU(2) break;
+    case 3: TFM_DS_GU(3) break;
+    case 4: TFM_DS_GU(4) break;
+    default: fail(TFM_E_UNSUPPORTED, "decode gate/up: hidden width");
+  }
+#undef TFM_DS_GU
+#undef TFM_DS_GU_X
+#undef TFM_DS_GU_P
+  check_hip(hipGetLastError(), "decode gate/up launch");
+}
+
+void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,
+                    const Grouping& g, const int32_t* meta, float* P, hipStream_t s) {
+  (void)meta;
+  DsDownArgs A{};
+  A.h = hsorted; A.E = g.E; A.H = H; A.I = I; A.down = down; A.slots = g.slots;
+  A.gates_sorted = g.gates_sorted; A.P = P;
+  const int nt = ds_down_lds(I, 1024) <= 160 * 1024 - 4096 ? ds_threads() : 256;
+  const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
+  const size_t lds = ds_down_lds(I, nt);
+  switch (I / 512) {
+#define TFM_DS_DN_P(CV, RV, NV, PV)                                                                      \
+  allow_lds(ds_down_kernel<CV, RV, NV, PV>, lds);                                                        \
+  ds_down_kernel<CV, RV, NV, PV><<<ds_grid(ds_down_kernel<CV, RV, NV, PV>, NV, lds,                      \
+                                           (int64_t)max_active * ((H + 4 * RV - 1) / (4 * RV))), NV, lds, s>>>(A);
+#define TFM_DS_DN_N(CV, RV, NV) \
+  if (pipe == 2 && NV == 256) { TFM_DS_DN_P(CV, RV, 256, 2) } else { TFM_DS_DN_P(CV, RV, NV, 1) }
+#define TFM_DS_DN(CV, RV) \
+  if (nt == 1024) { TFM_DS_DN_N(CV, RV, 1024) } else { TFM_DS_DN_N(CV, RV, 256) }
+    case 1: TFM_DS_DN(1, 4) break;
+    case 2: TFM_DS_DN(2, 2) break;
+    case 3: TFM_DS_DN(3, 1) break;
+    case 4: TFM_DS_DN(4, 1) break;
+#undef TFM_DS_DN
+#undef TFM_DS_DN_N
+#undef TFM_DS_DN_P
+    default: fail(TFM_E_UNSUPPORTED, "decode down: intermediate width");
+  }
+  check_hip(hipGetLastError(), "decode down launch");
+}
+
+}  // namespace tfm

@@ -41,6 +41,7 @@ struct WsHeader {
   uint32_t status;   // TFM_STATUS_* bits, sticky until tfm_status_word reads them
   uint32_t pad[63];
 };
+static_assert(sizeof(WsHeader) == 256, "workspace header size");
 
 // Grouping results shared by every consumer of a route list.
 struct Grouping {
@@ -94,6 +95,26 @@ void launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int 
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s);
+void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
+                          int E, uint16_t* logits, hipStream_t s);
+
+// Streaming decode path (dstream.hip). decode_stream_fits: the shapes it
+// has variants for. ds_topk_group ranks every token and publishes the
+// grouping with g.slots, g.gates_sorted and meta[0] = active slot count;
+// ds_gateup and ds_down read them.
+bool decode_stream_fits(int T, int K, int E, int H, int I);
+void launch_ds_topk_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                          float* gates, const Grouping& g, int32_t* meta, uint32_t* status,
+                          hipStream_t s);
+// The same grouping for given routes (ids [T*K], fp32 gates [T*K]).
+void launch_ds_group_given(const int32_t* idx, const float* gates, int T, int E, int K, const Grouping& g,
+                           int32_t* meta, uint32_t* status, hipStream_t s);
+void launch_ds_gateup(const uint16_t* x, int T, int K, int H, int I, int max_active,
+                      const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
+                      const int32_t* meta, uint16_t* h, hipStream_t s);
+void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,
+                    const Grouping& g, const int32_t* meta, float* P, hipStream_t s);
+
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
 void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
