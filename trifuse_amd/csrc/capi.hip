@@ -122,7 +122,6 @@ struct BlockWs {
   int4* slots;    // decode: per active slot {expert, first route, end route, 0}
   float* gates_sorted;  // decode: gates in sorted order
   uint16_t* xn;         // RMSNorm-ed input [T, H] (tfm_moe_forward_rmsnorm)
-  int32_t* meta;        // decode: [0] = active slot count
   size_t bytes;
 };
 
@@ -147,7 +146,6 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.slots = c.take<int4>((size_t)g.num_experts);
   w.gates_sorted = c.take<float>((size_t)R);
   w.xn = c.take<uint16_t>((size_t)(T * g.hidden_size));
-  w.meta = c.take<int32_t>(64);
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -234,17 +232,20 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     gd.slots = ws.slots;
     gd.gates_sorted = ws.gates_sorted;
     {
-      StageScope st(TFM_STAGE_GROUP, s);
-      launch_ds_group_given(idx, gates, (int)T, E, K, gd, ws.meta, &ws.hdr->status, s);
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ds_gateup(kDsGivenRoutes, x, nullptr, const_cast<int32_t*>(idx), const_cast<float*>(gates),
+                       (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s);
+    }
+    if (decode_small((int)T, K)) {
+      StageScope st(TFM_STAGE_DOWN, s);
+      launch_ds_down_combine(ws.h, idx, gates, ws.grp.inverse, (int)T, K, E, H, I, w->down, residual,
+                             g.residual_multiplier, y, s);
+      return;
     }
     const int max_active = (int)(R < E ? R : E);
     {
-      StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ds_gateup(x, (int)T, K, H, I, max_active, w->gate, w->up, gd, ws.meta, ws.h, s);
-    }
-    {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down(ws.h, H, I, max_active, w->down, gd, ws.meta, ws.P, s);
+      launch_ds_down(ws.h, H, I, max_active, w->down, gd, ws.P, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
     launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
@@ -522,21 +523,22 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
                            weights->logit_bias, T, H, E, ws.logits, s);
     }
     {
-      StageScope st(TFM_STAGE_TOPK, s);
-      launch_ds_topk_group(g.route, ws.logits, T, E, K, ws.idx, ws.gates, gd, ws.meta,
-                           &ws.hdr->status, s);
+      // Top-k and grouping run in this kernel's prologue.
+      StageScope st(TFM_STAGE_GATEUP, s);
+      launch_ds_gateup(g.route, static_cast<const uint16_t*>(x), ws.logits, ws.idx, ws.gates, T, K, E, H,
+                       I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s);
     }
     const int max_active = (int)(R < E ? R : E);
-    {
-      StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ds_gateup(static_cast<const uint16_t*>(x), T, K, H, I, max_active, weights->gate,
-                       weights->up, gd, ws.meta, ws.h, s);
-    }
-    {
+    if (decode_small(T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down(ws.h, H, I, max_active, weights->down, gd, ws.meta, ws.P, s);
-    }
-    {
+      launch_ds_down_combine(ws.h, ws.idx, ws.gates, ws.grp.inverse, T, K, E, H, I, weights->down,
+                             static_cast<const uint16_t*>(residual), g.residual_multiplier,
+                             static_cast<uint16_t*>(y), s);
+    } else {
+      {
+        StageScope st(TFM_STAGE_DOWN, s);
+        launch_ds_down(ws.h, H, I, max_active, weights->down, gd, ws.P, s);
+      }
       StageScope st(TFM_STAGE_COMBINE, s);
       launch_combine_sorted(ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
                             static_cast<const uint16_t*>(residual), g.residual_multiplier,

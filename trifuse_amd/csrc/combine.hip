@@ -70,11 +70,13 @@ __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __rest
 #pragma unroll
     for (int v = 0; v < 8; ++v) r[v] = 0.0f;
   }
+  // y = bf16(fma(rm, sum, residual)), the rounding the fused small-batch
+  // decode kernel (dstream.hip) reproduces.
   uint4 o;
-  o.x = pack_bf16x2(r[0] + rmul * s[0], r[1] + rmul * s[1]);
-  o.y = pack_bf16x2(r[2] + rmul * s[2], r[3] + rmul * s[3]);
-  o.z = pack_bf16x2(r[4] + rmul * s[4], r[5] + rmul * s[5]);
-  o.w = pack_bf16x2(r[6] + rmul * s[6], r[7] + rmul * s[7]);
+  o.x = pack_bf16x2(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
+  o.y = pack_bf16x2(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
+  o.z = pack_bf16x2(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
+  o.w = pack_bf16x2(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
   *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
 }
 
@@ -130,11 +132,13 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __res
 #pragma unroll
     for (int v = 0; v < 8; ++v) r[v] = 0.0f;
   }
+  // y = bf16(fma(rm, sum, residual)), the rounding the fused small-batch
+  // decode kernel (dstream.hip) reproduces.
   uint4 o;
-  o.x = pack_bf16x2(r[0] + rmul * s[0], r[1] + rmul * s[1]);
-  o.y = pack_bf16x2(r[2] + rmul * s[2], r[3] + rmul * s[3]);
-  o.z = pack_bf16x2(r[4] + rmul * s[4], r[5] + rmul * s[5]);
-  o.w = pack_bf16x2(r[6] + rmul * s[6], r[7] + rmul * s[7]);
+  o.x = pack_bf16x2(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
+  o.y = pack_bf16x2(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
+  o.z = pack_bf16x2(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
+  o.w = pack_bf16x2(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
   *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
 }
 

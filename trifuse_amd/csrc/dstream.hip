@@ -35,6 +35,7 @@
 namespace tfm {
 
 constexpr int kDsCostUnpack = 2;  // item cost = kDsCostUnpack + routes of its expert
+constexpr int kDsSmallT = 2;      // tokens up to which the three-kernel layer is used
 constexpr int kDsDownXB = 4;      // h rows staged per wave in the down kernel
 
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
@@ -97,37 +98,49 @@ __device__ __forceinline__ void wave_range(int4 sl, int ipe, int gw, int nw, Wav
 }
 
 // ---------------------------------------------------------------------------
-// 2. Top-k of every token and the stable grouping of the T*K routes.
-// One workgroup of 16 waves; wave w ranks tokens w, w+16, ...; the first four
-// waves then group (one thread per route). MODE kDsGiven takes the routes
-// (ids and fp32 gates) from idx/gates instead of ranking: ids outside [0, E)
-// sort after every valid id (bucket E), are left out of the slot table and
-// set TFM_STATUS_BAD_EXPERT_ID.
-constexpr int kDsGiven = 2;
+// 2. Routing and grouping (in the gate/up kernel's prologue).
+constexpr int kDsGiven = kDsGivenRoutes;  // routes given (idx, fp32 gates) instead of ranked
 
+// LDS of the in-workgroup routing and grouping.
+struct DsGroupLds {
+  int e[256];       // route -> bucket (expert, E for a bad id)
+  float g[256];     // route -> fp32 gate
+  int wcnt[4][65];  // per grouping wave: routes per bucket
+  int wpre[4][65];  // per grouping wave: first position per bucket
+  int off[66];      // bucket offsets
+  int act[65];      // active experts ascending; act[E] = count
+  int order[256];   // sorted position -> flat route
+};
+
+// Routing and stable grouping of the T*K routes of every token, inside one
+// workgroup of at least 4 waves (R = T*K <= 256). MODE OLMOE/GRANITE ranks
+// the logits [T, E] (route_wave.h; waves take tokens round-robin); kDsGiven
+// takes the routes (ids and fp32 gates) from idx/gates instead: ids outside
+// [0, E) sort after every valid id (bucket E), are left out of the active
+// list and set TFM_STATUS_BAD_EXPERT_ID. The position of route f is the
+// number of routes to lower buckets plus the routes to its bucket with a
+// lower flat index. Results land in L (the caller synchronises before reading
+// them); with `publish`, also in the workspace: flat idx/gates (ranked
+// modes), order, inverse, offsets, active list, sorted gates, the slot table
+// {expert, first route, end route, active count} and the status word.
 template <int MODE>
-__device__ __forceinline__ void ds_rank_group(const uint16_t* __restrict__ logits, int T, int E, int K,
-                                              int32_t* __restrict__ idx, float* __restrict__ gates,
-                                              const Grouping& g, int32_t* __restrict__ meta,
+__device__ __forceinline__ void ds_rank_group(DsGroupLds& L, const uint16_t* __restrict__ logits, int T,
+                                              int E, int K, int32_t* __restrict__ idx,
+                                              float* __restrict__ gates, bool publish, const Grouping& g,
                                               uint32_t* __restrict__ status) {
-  __shared__ int s_e[256];
-  __shared__ float s_g[256];
-  __shared__ int wcnt[4][65];
-  __shared__ int wpre[4][65];
-  __shared__ int s_off[66];
-  __shared__ int s_act[65];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
   const int R = T * K;
   if (MODE == kDsGiven) {
     if (tid < R) {
       const int id = idx[tid];
-      s_e[tid] = (id < 0 || id >= E) ? E : id;
-      s_g[tid] = gates[tid];
+      L.e[tid] = (id < 0 || id >= E) ? E : id;
+      L.g[tid] = gates[tid];
     }
   } else {
-    for (int t = wave; t < T; t += 16) {
+    for (int t = wave; t < T; t += nwaves) {
       const uint16_t* row = logits + (int64_t)t * E;
       float gv;
       int id;
@@ -138,19 +151,19 @@ __device__ __forceinline__ void ds_rank_group(const uint16_t* __restrict__ logit
         id = granite_route_wave(row, E, K, &gv);
       }
       if (lane < K) {
-        s_e[t * K + lane] = id;
-        s_g[t * K + lane] = gv;
-        idx[(int64_t)t * K + lane] = id;
-        gates[(int64_t)t * K + lane] = gv;
+        L.e[t * K + lane] = id;
+        L.g[t * K + lane] = gv;
+        if (publish) {
+          idx[(int64_t)t * K + lane] = id;
+          gates[(int64_t)t * K + lane] = gv;
+        }
       }
     }
   }
-  if (tid < 4 * 65) (&wcnt[0][0])[tid] = 0;
+  for (int i = tid; i < 4 * 65; i += blockDim.x) (&L.wcnt[0][0])[i] = 0;
   __syncthreads();
-  // Stable grouping: position of route f = routes to lower buckets + routes
-  // to its bucket with a lower flat index (buckets 0..E, E = bad ids).
   const bool live = tid < R;
-  const int e = live ? s_e[tid] : 0;
+  const int e = live ? L.e[tid] : 0;
   int rank_w = 0;
   if (wave < 4) {
     uint64_t match = __ballot(live);
@@ -162,66 +175,58 @@ __device__ __forceinline__ void ds_rank_group(const uint16_t* __restrict__ logit
     }
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     rank_w = __popcll(match & lt);
-    if (live && rank_w == 0) wcnt[wave][e] = __popcll(match);
+    if (live && rank_w == 0) L.wcnt[wave][e] = __popcll(match);
   }
   __syncthreads();
   if (wave == 0) {
     // Lanes 0..63 hold experts 0..63; the bad bucket E (<= 64) comes last.
-    const int c0 = wcnt[0][lane], c1 = wcnt[1][lane], c2 = wcnt[2][lane], c3 = wcnt[3][lane];
+    const int c0 = L.wcnt[0][lane], c1 = L.wcnt[1][lane], c2 = L.wcnt[2][lane], c3 = L.wcnt[3][lane];
     const int cnt = lane < E ? c0 + c1 + c2 + c3 : 0;
     const int incl = wave_incl_scan(cnt);
     const int excl = incl - cnt;
     if (lane < E) {
-      s_off[lane] = excl;
-      wpre[0][lane] = excl;
-      wpre[1][lane] = excl + c0;
-      wpre[2][lane] = excl + c0 + c1;
-      wpre[3][lane] = excl + c0 + c1 + c2;
+      L.off[lane] = excl;
+      L.wpre[0][lane] = excl;
+      L.wpre[1][lane] = excl + c0;
+      L.wpre[2][lane] = excl + c0 + c1;
+      L.wpre[3][lane] = excl + c0 + c1 + c2;
     }
     if (lane == 63) {
-      s_off[E] = incl;
+      L.off[E] = incl;
       int b = incl;
-      wpre[0][E] = b; b += wcnt[0][E];
-      wpre[1][E] = b; b += wcnt[1][E];
-      wpre[2][E] = b; b += wcnt[2][E];
-      wpre[3][E] = b;
-      s_off[E + 1] = b + wcnt[3][E];  // == R
+      L.wpre[0][E] = b; b += L.wcnt[0][E];
+      L.wpre[1][E] = b; b += L.wcnt[1][E];
+      L.wpre[2][E] = b; b += L.wcnt[2][E];
+      L.wpre[3][E] = b;
+      L.off[E + 1] = b + L.wcnt[3][E];  // == R
     }
     const uint64_t act = __ballot(lane < E && cnt > 0);
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    if (lane < E && cnt > 0) s_act[__popcll(act & lt)] = lane;
-    if (lane == 0) s_act[E] = __popcll(act);
+    if (lane < E && cnt > 0) L.act[__popcll(act & lt)] = lane;
+    if (lane == 0) L.act[E] = __popcll(act);
   }
   __syncthreads();
   if (live) {
-    const int pos = wpre[wave][e] + rank_w;
-    g.order[pos] = tid;
-    g.inverse[tid] = pos;
-    g.gates_sorted[pos] = s_g[tid];
+    const int pos = L.wpre[wave][e] + rank_w;
+    L.order[pos] = tid;
+    if (publish) {
+      g.order[pos] = tid;
+      g.inverse[tid] = pos;
+      g.gates_sorted[pos] = L.g[tid];
+    }
   }
-  const int U = s_act[E];
-  if (tid <= E) {
-    g.offsets[tid] = s_off[tid];
-    if (tid == E || tid < U) g.active[tid] = s_act[tid];
+  if (publish) {
+    const int U = L.act[E];
+    if (tid <= E) {
+      g.offsets[tid] = L.off[tid];
+      if (tid == E || tid < U) g.active[tid] = L.act[tid];
+    }
+    if (tid < E) {
+      const int ex = tid < U ? L.act[tid] : -1;
+      g.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, U) : make_int4(ex, L.off[ex], L.off[ex + 1], U);
+    }
+    if (tid == 0) *status = L.off[E] < R ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
   }
-  if (tid < E) {
-    const int ex = tid < U ? s_act[tid] : -1;
-    g.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, U) : make_int4(ex, s_off[ex], s_off[ex + 1], U);
-  }
-  if (tid == 0) {
-    meta[0] = U;
-    *status = s_off[E] < R ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
-  }
-}
-
-template <int MODE>
-__global__ __launch_bounds__(1024) void ds_topk_group_kernel(const uint16_t* __restrict__ logits,
-                                                             int T, int E, int K,
-                                                             int32_t* __restrict__ idx,
-                                                             float* __restrict__ gates,
-                                                             Grouping g, int32_t* __restrict__ meta,
-                                                             uint32_t* __restrict__ status) {
-  ds_rank_group<MODE>(logits, T, E, K, idx, gates, g, meta, status);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,11 +306,14 @@ __device__ __forceinline__ void ds_stage_chunk(const uint16_t* __restrict__ src,
 // items are in flight per wave: the loads of item i+2 go out as soon as the
 // dot products of item i have consumed its registers.
 struct DsGateUpArgs {
-  const uint16_t* x;  // [T, H]
+  const uint16_t* x;       // [T, H]
+  const uint16_t* logits;  // [T, E] (ranked modes)
+  int32_t* idx;            // [T*K] flat route ids: written (ranked) or read (given)
+  float* gates;            // [T*K] flat fp32 gates: written (ranked) or read (given)
   int T, K, E, H, I;
   tfm_affine gate, up;
-  const int4* slots;  // [E] {expert, first route, end route, active count}
-  const int32_t* order;
+  Grouping grp;            // published by workgroup 0, with slots and gates_sorted
+  uint32_t* status;
   uint16_t* h;  // [R, I]
 };
 
@@ -357,26 +365,32 @@ __device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restr
   }
 }
 
-template <int C, int XCH, int NT, int PIPE>
+template <int C, int XCH, int NT, int PIPE, int MODE>
 __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
   extern __shared__ uint4 ds_lds[];
-  const int H = A.H, N = A.I, T = A.T, K = A.K;
+  const int H = A.H, N = A.I, T = A.T, K = A.K, E = A.E;
   const int R = T * K;
   constexpr int nch = 16 * C;
+  // Dynamic LDS: the grouping's scratch, later overwritten by the staged x
+  // rows, then the route tokens (ds_gateup_lds sizes it).
+  DsGroupLds& GL = *reinterpret_cast<DsGroupLds*>(ds_lds);
   uint4* xs = ds_lds;                                        // [T][4][nch]
   float* xsum = reinterpret_cast<float*>(xs + T * 4 * nch);  // [T][nch]
-  int* s_tok = reinterpret_cast<int*>(xsum + T * nch);       // [R]
+  const int xbytes = T * nch * 68;
+  int* s_tok = reinterpret_cast<int*>(reinterpret_cast<char*>(ds_lds) +
+                                      (xbytes > (int)sizeof(DsGroupLds) ? xbytes : (int)sizeof(DsGroupLds)));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int ll = lane & 15, rsub = lane >> 4;
   const int gw = blockIdx.x * (NT / 64) + (tid >> 6), nw = gridDim.x * (NT / 64);
 
-  // Prologue, ordered so that its memory latencies overlap: the slot table,
-  // the x rows of every token (at most XCH 32-element chunks per thread) and
-  // the route tokens are requested first; the first two items'
-  // weights as soon as the slot table is in; the x rows are permuted into
-  // dot2 pair order and stored while those weights are in flight.
-  const int4 sl = load_slot(A.slots, A.E);
+  // Prologue. The x rows of every token (at most XCH 32-element chunks per
+  // thread) are requested first; every workgroup then routes and groups the
+  // T*K routes itself (a few hundred VALU operations, cheaper than one more
+  // dependent kernel launch) and workgroup 0 publishes the result for the
+  // down projection and the combine. The first items' weights go out as soon
+  // as the grouping is known; the x rows are permuted into dot2 pair order
+  // and stored while those weights are in flight.
   uint4 xr[XCH][4];
 #pragma unroll
   for (int u = 0; u < XCH; ++u) {
@@ -387,7 +401,18 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
       for (int v = 0; v < 4; ++v) xr[u][v] = src[v];
     }
   }
-  const int otok = tid < R ? A.order[tid] : 0;
+  ds_rank_group<MODE>(GL, A.logits, T, E, K, A.idx, A.gates, blockIdx.x == 0, A.grp, A.status);
+  __syncthreads();
+  int4 sl = make_int4(-1, 0, 0, 0);
+  {
+    const int U = GL.act[E];
+    if (lane < U) {
+      const int ex = GL.act[lane];
+      sl = make_int4(ex, GL.off[ex], GL.off[ex + 1], U);
+    } else {
+      sl.w = U;
+    }
+  }
   WaveRange wr;
   const int ipe = (N + 3) / 4;
   wave_range(sl, ipe, gw, nw, wr);
@@ -401,7 +426,8 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
   DsGU<C> wA, wB;
   if (wr.i0 < wr.i1) load(wA, wr.i0);
   if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
-  if (tid < R) s_tok[tid] = otok / K;
+  for (int j = tid; j < R; j += NT) s_tok[j] = GL.order[j] / K;
+  __syncthreads();  // the grouping scratch is read; the x rows may overwrite it
 #pragma unroll
   for (int u = 0; u < XCH; ++u) {
     const int p = tid + NT * u;
@@ -581,6 +607,96 @@ __global__ __launch_bounds__(NT) void ds_down_kernel(DsDownArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// Small batches (T <= kDsSmallT): the down GEMV fused with the combine.
+
+// 4+5 for few tokens: y[t, n] = bf16(fma(rm, sum_k gate_{t,k} * (h_{t,k} . down_n), res[t, n]))
+// with the products and the k-ordered sum rounded exactly as ds_down_kernel
+// followed by combine_sorted_kernel round them. A workgroup owns a block of
+// 4 output rows: it stages the h rows of every route in LDS, wave w computes
+// the rows' products for routes w, w+4, .. (streaming the rows' weights of
+// each routed expert), and wave 0 sums each token's K products in k order.
+struct DsDownCombineArgs {
+  const uint16_t* h;        // [R, I] sorted rows
+  const int32_t* idx;       // [R] flat route -> expert
+  const float* gates;       // [R] flat route gates
+  const int32_t* inverse;   // [R] flat route -> sorted position
+  int T, K, E, H, I;
+  tfm_affine down;
+  const uint16_t* residual;  // [T, H] or null
+  float rmul;
+  uint16_t* y;  // [T, H]
+};
+
+constexpr int kDsSmallR = 16;  // routes of the small-batch layer
+
+template <int C>
+__global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs A) {
+  extern __shared__ uint4 ds_lds[];
+  __shared__ float s_p[kDsSmallR][4];  // product of route f for row 4*blockIdx.x + r
+  constexpr int nch = 16 * C;
+  constexpr int FW = kDsSmallR / 4;    // routes per wave
+  const int T = A.T, K = A.K, E = A.E, N = A.H, kin = A.I;
+  const int R = T * K;
+  uint4* xs = ds_lds;                                        // [R][4][nch]
+  float* xsum = reinterpret_cast<float*>(xs + R * 4 * nch);  // [R][nch]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int ll = lane & 15, rsub = lane >> 4;
+  const int n = blockIdx.x * 4 + rsub;
+  int fe = -1, fpos = 0;
+  float fg = 0.0f;
+  if (lane < R) {
+    fe = A.idx[lane];
+    fg = A.gates[lane];
+    fpos = A.inverse[lane];
+  }
+  // This wave's routes' weight rows, then every route's h row (sorted
+  // position inverse[f]) into slot f. Bad routes' h rows were never written:
+  // they are staged but not used.
+  DsDn<C, 1> wt[FW];
+#pragma unroll
+  for (int u = 0; u < FW; ++u) {
+    const int f = wave + 4 * u;
+    const int e = uni(readlane_i(fe, min(f, R - 1)));
+    if (f < R && e >= 0 && e < E) ds_load_row<C>(ds_mat(A.down, e, N, kin), n, kin, ll, wt[u].r[0]);
+  }
+  for (int p = tid; p < R * nch; p += 256) {
+    const int f = p / nch, k = p % nch;
+    const int pos = __shfl(fpos, f, 64);
+    ds_stage_chunk(A.h + (int64_t)pos * kin + 32 * k, xs, xsum, f, k, nch);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < FW; ++u) {
+    const int f = wave + 4 * u;
+    if (f >= R) break;
+    const int e = uni(readlane_i(fe, f));
+    float pr = 0.0f;
+    if (e >= 0 && e < E) {
+      float acc[1];
+      ds_dn_dot<C, 1>(wt[u], xs, xsum, f, ll, acc);
+      const float sum = dpp_group_sum<16>(acc[0]);
+      const float gt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fg), f));
+      pr = __fmul_rn(sum, gt);
+    }
+    if (ll == 0) s_p[f][rsub] = pr;
+  }
+  __syncthreads();
+  if (wave == 0 && ll == 0 && n < N) {
+    for (int t = 0; t < T; ++t) {
+      float sacc = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const int f = t * K + k;
+        const int e = A.idx[f];
+        if (e >= 0 && e < E) sacc = __fadd_rn(sacc, s_p[f][rsub]);
+      }
+      const float r = A.residual ? bf2f(A.residual[(int64_t)t * N + n]) : 0.0f;
+      A.y[(int64_t)t * N + n] = (uint16_t)pack_bf16x2(__builtin_fmaf(A.rmul, sacc, r), 0.0f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 static int device_cus() {
@@ -605,8 +721,8 @@ static int env_int(const char* name, int dflt, int lo, int hi) {
 }
 
 static size_t ds_gateup_lds(int T, int K, int H) {
-  const int nch = H / 32;
-  return (size_t)T * nch * 4 * 16 + (size_t)T * nch * 4 + (size_t)T * K * 4;
+  const size_t x = (size_t)T * (H / 32) * 68;  // staged x rows and their chunk sums
+  return std::max(x, sizeof(DsGroupLds)) + (size_t)T * K * 4;
 }
 
 static size_t ds_down_lds(int I, int threads) {
@@ -619,25 +735,6 @@ bool decode_stream_fits(int T, int K, int E, int H, int I) {
   return w_ok && E <= 64 && T * K <= 256 && T >= 1 && T * (H / 32) <= 256 * kDsXChunks &&
          ds_gateup_lds(T, K, H) <= 64 * 1024 &&
          ds_down_lds(I, 256) <= 64 * 1024;
-}
-
-void launch_ds_topk_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
-                          float* gates, const Grouping& g, int32_t* meta, uint32_t* status,
-                          hipStream_t s) {
-  if (T * K > 256 || E > 64) fail(TFM_E_INVALID, "decode top-k/grouping: more than 256 routes or 64 experts");
-  if (route_kind == TFM_ROUTE_OLMOE)
-    ds_topk_group_kernel<TFM_ROUTE_OLMOE><<<1, 1024, 0, s>>>(logits, T, E, K, idx, gates, g, meta, status);
-  else
-    ds_topk_group_kernel<TFM_ROUTE_GRANITE><<<1, 1024, 0, s>>>(logits, T, E, K, idx, gates, g, meta, status);
-  check_hip(hipGetLastError(), "decode top-k/grouping launch");
-}
-
-void launch_ds_group_given(const int32_t* idx, const float* gates, int T, int E, int K, const Grouping& g,
-                           int32_t* meta, uint32_t* status, hipStream_t s) {
-  if (T * K > 256 || E > 64) fail(TFM_E_INVALID, "decode grouping: more than 256 routes or 64 experts");
-  ds_topk_group_kernel<kDsGiven><<<1, 1024, 0, s>>>(nullptr, T, E, K, const_cast<int32_t*>(idx),
-                                                   const_cast<float*>(gates), g, meta, status);
-  check_hip(hipGetLastError(), "decode grouping launch");
 }
 
 // Workgroups resident per compute unit for a kernel at a block and dynamic
@@ -688,29 +785,36 @@ static void allow_lds(Kern kern, size_t lds) {
 // 1024 (one workgroup per compute unit) at decode shapes.
 static int ds_threads() { return env_int("TFM_DS_THREADS", 256, 256, 1024) >= 1024 ? 1024 : 256; }
 
-void launch_ds_gateup(const uint16_t* x, int T, int K, int H, int I, int max_active,
-                      const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
-                      const int32_t* meta, uint16_t* h, hipStream_t s) {
-  (void)meta;
+void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,
+                      int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,
+                      const Grouping& g, uint32_t* status, uint16_t* h, hipStream_t s) {
+  if (T * K > 256 || E > 64) fail(TFM_E_INVALID, "decode gate/up: more than 256 routes or 64 experts");
   DsGateUpArgs A{};
-  A.x = x; A.T = T; A.K = K; A.E = g.E; A.H = H; A.I = I; A.gate = gate; A.up = up;
-  A.slots = g.slots; A.order = g.order; A.h = h;
+  A.x = x; A.logits = logits; A.idx = idx; A.gates = gates;
+  A.T = T; A.K = K; A.E = E; A.H = H; A.I = I; A.gate = gate; A.up = up;
+  A.grp = g; A.status = status; A.h = h;
   const size_t lds = ds_gateup_lds(T, K, H);
+  const int max_active = T * K < E ? T * K : E;
   const int64_t items = (int64_t)max_active * ((I + 3) / 4);
   const int nt = ds_threads();
   const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
   const int per = T * (H / 32);
   const int xch = per <= nt ? 1 : per <= 2 * nt ? 2 : 4;
-#define TFM_DS_GU_P(CV, XV, NV, PV) \
-  ds_gateup_kernel<CV, XV, NV, PV><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV>, NV, lds, items), NV, lds, s>>>(A);
+#define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                              \
+  ds_gateup_kernel<CV, XV, NV, PV, MV><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV, MV>, NV, lds, items), \
+                                         NV, lds, s>>>(A);
+#define TFM_DS_GU_M(CV, XV, NV, PV)                                         \
+  if (mode == TFM_ROUTE_OLMOE) { TFM_DS_GU_P(CV, XV, NV, PV, TFM_ROUTE_OLMOE) }     \
+  else if (mode == TFM_ROUTE_GRANITE) { TFM_DS_GU_P(CV, XV, NV, PV, TFM_ROUTE_GRANITE) } \
+  else { TFM_DS_GU_P(CV, XV, NV, PV, kDsGiven) }
 #define TFM_DS_GU_X(CV, XV, NV) \
-  if (pipe == 2 && NV == 256) { TFM_DS_GU_P(CV, XV, 256, 2) } else { TFM_DS_GU_P(CV, XV, NV, 1) }
+  if (pipe == 2 && NV == 256) { TFM_DS_GU_M(CV, XV, 256, 2) } else { TFM_DS_GU_M(CV, XV, NV, 1) }
 #define TFM_DS_GU(CV)                                           \
   if (nt == 1024) {                                             \
-    if (xch == 1) TFM_DS_GU_X(CV, 1, 1024) else TFM_DS_GU_X(CV, 2, 1024) \
-  } else if (xch == 1) TFM_DS_GU_X(CV, 1, 256)                  \
-  else if (xch == 2) TFM_DS_GU_X(CV, 2, 256)                    \
-  else TFM_DS_GU_X(CV, 4, 256)
+    if (xch == 1) { TFM_DS_GU_X(CV, 1, 1024) } else { TFM_DS_GU_X(CV, 2, 1024) } \
+  } else if (xch == 1) { TFM_DS_GU_X(CV, 1, 256) }              \
+  else if (xch == 2) { TFM_DS_GU_X(CV, 2, 256) }                \
+  else { TFM_DS_GU_X(CV, 4, 256) }
   switch (H / 512) {
     case 1: TFM_DS_GU(1) break;
     case 2: TFM_DS_GU(2) break;
@@ -720,13 +824,13 @@ void launch_ds_gateup(const uint16_t* x, int T, int K, int H, int I, int max_act
   }
 #undef TFM_DS_GU
 #undef TFM_DS_GU_X
+#undef TFM_DS_GU_M
 #undef TFM_DS_GU_P
   check_hip(hipGetLastError(), "decode gate/up launch");
 }
 
 void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,
-                    const Grouping& g, const int32_t* meta, float* P, hipStream_t s) {
-  (void)meta;
+                    const Grouping& g, float* P, hipStream_t s) {
   DsDownArgs A{};
   A.h = hsorted; A.E = g.E; A.H = H; A.I = I; A.down = down; A.slots = g.slots;
   A.gates_sorted = g.gates_sorted; A.P = P;
@@ -752,6 +856,34 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
     default: fail(TFM_E_UNSUPPORTED, "decode down: intermediate width");
   }
   check_hip(hipGetLastError(), "decode down launch");
+}
+
+// At most kDsSmallT tokens and kDsSmallR routes (every route's h row is
+// staged in LDS, and each route's data sits in one lane).
+bool decode_small(int T, int K) { return T >= 1 && T <= kDsSmallT && T * K <= kDsSmallR; }
+
+void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,
+                            const int32_t* inverse, int T, int K, int E, int H, int I, const tfm_affine& down,
+                            const uint16_t* residual, float rmul, uint16_t* y, hipStream_t s) {
+  if (!decode_small(T, K)) fail(TFM_E_INVALID, "decode down+combine: batch too large");
+  DsDownCombineArgs A{};
+  A.h = hsorted; A.idx = idx; A.gates = gates; A.inverse = inverse;
+  A.T = T; A.K = K; A.E = E; A.H = H; A.I = I; A.down = down; A.residual = residual; A.rmul = rmul; A.y = y;
+  const int R = T * K;
+  const size_t lds = (size_t)R * (I / 32) * 68;
+  const unsigned grid = (unsigned)((H + 3) / 4);
+#define TFM_DS_DC(CV)                                \
+  allow_lds(ds_down_combine_kernel<CV>, lds);        \
+  ds_down_combine_kernel<CV><<<grid, 256, lds, s>>>(A);
+  switch (I / 512) {
+    case 1: TFM_DS_DC(1) break;
+    case 2: TFM_DS_DC(2) break;
+    case 3: TFM_DS_DC(3) break;
+    case 4: TFM_DS_DC(4) break;
+    default: fail(TFM_E_UNSUPPORTED, "decode down+combine: intermediate width");
+  }
+#undef TFM_DS_DC
+  check_hip(hipGetLastError(), "decode down+combine launch");
 }
 
 }  // namespace tfm

@@ -23,24 +23,43 @@ namespace tfm {
 // normaliser 1/sum. Order of arithmetic: max by compare-select from -FLT_MAX
 // (NaN skipped), e = exp(l - max) with route_expf, the sum as four-value
 // chunks (each summed in order) combined by the natural pairwise tree, and
-// p = e * (1/sum) (MLXOLMoERouter.h:26-61).
+// p = e * (1/sum) (MLXOLMoERouter.h:26-61). The cross-lane steps are DPP
+// moves: the maximum is exact in any order, and each tree level adds the two
+// operands the xor-partner tree adds (the quads, then half-rows, then rows
+// hold equal values), so the result is that tree's bit for bit.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_f(float v) {
+  const int s = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+  return fmaxf(v, __int_as_float(s));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float wave_softmax_exp(float ld, float* norm) {
   float m = -3.40282347e38f;
   m = m < ld ? ld : m;
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) m = fmaxf(m, shfl_xor_f(m, k));
+  m = dpp_max_f<0xb1, 0xf>(m);   // quad_perm [1,0,3,2]
+  m = dpp_max_f<0x4e, 0xf>(m);   // quad_perm [2,3,0,1]
+  m = dpp_max_f<0x141, 0xf>(m);  // row_half_mirror
+  m = dpp_max_f<0x140, 0xf>(m);  // row_mirror
+  m = dpp_max_f<0x142, 0xa>(m);  // row_bcast:15
+  m = dpp_max_f<0x143, 0xc>(m);  // row_bcast:31
+  m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
   const float ex = route_expf(ld - m);
-  const int lane = threadIdx.x & 63;
-  const int q0 = lane & ~3;
-  const float a0 = shfl_f(ex, q0), a1 = shfl_f(ex, q0 + 1), a2 = shfl_f(ex, q0 + 2),
-              a3 = shfl_f(ex, q0 + 3);
+  // Lane values of the quad: quad_perm [0,0,0,0] .. [3,3,3,3].
+  const float a0 = dpp_mov_f<0x00>(ex), a1 = dpp_mov_f<0x55>(ex), a2 = dpp_mov_f<0xaa>(ex),
+              a3 = dpp_mov_f<0xff>(ex);
   float s = a0 + a1;
   s = s + a2;
   s = s + a3;
-  s = s + shfl_xor_f(s, 4);
-  s = s + shfl_xor_f(s, 8);
-  s = s + shfl_xor_f(s, 16);
-  s = s + shfl_xor_f(s, 32);
+  s = dpp_plus<0x141, 0xf>(s);  // + quad l ^ 1 (xor 4)
+  s = dpp_plus<0x140, 0xf>(s);  // + half-row l ^ 1 (xor 8)
+  s = dpp_plus<0x142, 0xa>(s);  // + row l ^ 1 (xor 16), rows 1 and 3
+  s = dpp_plus<0x143, 0xc>(s);  // + rows 0-1 (xor 32), rows 2 and 3
+  s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
   *norm = 1.0f / s;
   return ex;
 }
@@ -91,8 +110,8 @@ __device__ __forceinline__ int olmoe_route_wave(const uint16_t* __restrict__ row
     const uint64_t m = __ballot(!removed && key == kmax);
     const int sel = __ffsll((unsigned long long)m) - 1;  // ties: lowest id
     // Slot `slot` goes to lane `slot` of the result.
-    const float g = __shfl(p, sel, 64);
-    const int gb = __shfl((int)pb, sel, 64);
+    const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), sel));
+    const int gb = __builtin_amdgcn_readlane((int)pb, sel);
     if (lane == slot) {
       my_idx = sel;
       my_gate = g;
@@ -122,7 +141,7 @@ __device__ __forceinline__ int granite_route_wave(const uint16_t* __restrict__ r
     const uint64_t m = __ballot(!removed && key == kmax);
     const int sel = 63 - __clzll((long long)m);  // ties: the higher id ranks higher
     const int slot = K - 1 - r;
-    const float sv = __shfl(v, sel, 64);
+    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), sel));
     if (lane == slot) {
       my_idx = sel;
       my_val = sv;

@@ -99,22 +99,26 @@ void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float
                           int E, uint16_t* logits, hipStream_t s);
 
 // Streaming decode path (dstream.hip). decode_stream_fits: the shapes it
-// has variants for. ds_topk_group ranks every token and publishes the
-// grouping with g.slots, g.gates_sorted and meta[0] = active slot count;
-// ds_gateup and ds_down read them.
+// has variants for. ds_gateup routes (mode TFM_ROUTE_OLMOE/GRANITE: ranks
+// logits [T,E] and writes idx/gates) or takes given routes (mode
+// kDsGivenRoutes: reads idx/gates), groups them, publishes the grouping
+// (g with g.slots and g.gates_sorted) and the status word, and writes the
+// SwiGLU rows h in sorted order; ds_down reads the published grouping.
+constexpr int kDsGivenRoutes = 2;
 bool decode_stream_fits(int T, int K, int E, int H, int I);
-void launch_ds_topk_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
-                          float* gates, const Grouping& g, int32_t* meta, uint32_t* status,
-                          hipStream_t s);
-// The same grouping for given routes (ids [T*K], fp32 gates [T*K]).
-void launch_ds_group_given(const int32_t* idx, const float* gates, int T, int E, int K, const Grouping& g,
-                           int32_t* meta, uint32_t* status, hipStream_t s);
-void launch_ds_gateup(const uint16_t* x, int T, int K, int H, int I, int max_active,
-                      const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
-                      const int32_t* meta, uint16_t* h, hipStream_t s);
+void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,
+                      int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,
+                      const Grouping& g, uint32_t* status, uint16_t* h, hipStream_t s);
 void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,
-                    const Grouping& g, const int32_t* meta, float* P, hipStream_t s);
+                    const Grouping& g, float* P, hipStream_t s);
 
+// Few tokens (decode_small): the down GEMV fused with the combine
+// (y[t] = bf16(fma(rm, sum_k gate * out, residual)), rounded as the
+// separate down GEMV and combine round it).
+bool decode_small(int T, int K);
+void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,
+                            const int32_t* inverse, int T, int K, int E, int H, int I, const tfm_affine& down,
+                            const uint16_t* residual, float rmul, uint16_t* y, hipStream_t s);
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
 void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
