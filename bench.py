@@ -228,7 +228,7 @@ def dominant_roofline(r: Runner, stages):
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
         achieved = per_launch / dur_s / 1e9
-        return {"kernel": "decode_gateup_kernel", "bound": "hbm", "achieved": achieved,
+        return {"kernel": "ds_gateup_kernel", "bound": "hbm", "achieved": achieved,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                 "traffic": None, "alg_bytes_per_launch": per_launch,
                 "us_per_launch": st["us_per_launch"]}

@@ -783,7 +783,10 @@ static void allow_lds(Kern kern, size_t lds) {
 
 // Threads per workgroup of the streaming GEMVs: 256 measured faster than
 // 1024 (one workgroup per compute unit) at decode shapes.
-static int ds_threads() { return env_int("TFM_DS_THREADS", 256, 256, 1024) >= 1024 ? 1024 : 256; }
+static int ds_threads() {
+  const int v = env_int("TFM_DS_THREADS", 256, 256, 1024);
+  return v >= 1024 ? 1024 : v >= 512 ? 512 : 256;
+}
 
 void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,
                       int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,
@@ -812,6 +815,8 @@ void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32
 #define TFM_DS_GU(CV)                                           \
   if (nt == 1024) {                                             \
     if (xch == 1) { TFM_DS_GU_X(CV, 1, 1024) } else { TFM_DS_GU_X(CV, 2, 1024) } \
+  } else if (nt == 512) {                                       \
+    if (xch == 1) { TFM_DS_GU_X(CV, 1, 512) } else { TFM_DS_GU_X(CV, 2, 512) } \
   } else if (xch == 1) { TFM_DS_GU_X(CV, 1, 256) }              \
   else if (xch == 2) { TFM_DS_GU_X(CV, 2, 256) }                \
   else { TFM_DS_GU_X(CV, 4, 256) }
@@ -845,7 +850,8 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
 #define TFM_DS_DN_N(CV, RV, NV) \
   if (pipe == 2 && NV == 256) { TFM_DS_DN_P(CV, RV, 256, 2) } else { TFM_DS_DN_P(CV, RV, NV, 1) }
 #define TFM_DS_DN(CV, RV) \
-  if (nt == 1024) { TFM_DS_DN_N(CV, RV, 1024) } else { TFM_DS_DN_N(CV, RV, 256) }
+  if (nt == 1024) { TFM_DS_DN_N(CV, RV, 1024) } else if (nt == 512) { TFM_DS_DN_N(CV, RV, 512) } \
+  else { TFM_DS_DN_N(CV, RV, 256) }
     case 1: TFM_DS_DN(1, 4) break;
     case 2: TFM_DS_DN(2, 2) break;
     case 3: TFM_DS_DN(3, 1) break;
