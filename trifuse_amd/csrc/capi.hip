@@ -142,7 +142,7 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.P = c.take<float>((size_t)(R * g.hidden_size));
   const int64_t chunks = std::max<int64_t>(group_blocks(R, kGroupChunk),
                                            group_blocks(R, kTopkTokensPerBlock * g.experts_per_token));
-  w.hist = c.take<int32_t>((size_t)((chunks + 1) * (g.num_experts + 1)));
+  w.hist = c.take<int32_t>((size_t)group_hist_rows(chunks) * (g.num_experts + 1));
   w.slots = c.take<int4>((size_t)g.num_experts);
   w.gates_sorted = c.take<float>((size_t)R);
   w.xn = c.take<uint16_t>((size_t)(T * g.hidden_size));
@@ -173,7 +173,7 @@ static GroupWs carve_group(int64_t n, int E, void* base) {
   w.grp.offsets = c.take<int32_t>((size_t)E + 1);
   w.grp.active = c.take<int32_t>((size_t)E + 1);
   w.grp.E = E;
-  w.hist = c.take<int32_t>((size_t)((group_blocks(n, kGroupChunk) + 1) * (E + 1)));
+  w.hist = c.take<int32_t>((size_t)group_hist_rows(group_blocks(n, kGroupChunk)) * (E + 1));
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -670,7 +670,7 @@ size_t tfm_expert_routes_workspace_bytes(const tfm_plan* plan, int64_t n_routes)
   c.take<int32_t>((size_t)g.num_experts + 1);  // active
   c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
   c.take<float>((size_t)(n_routes * g.hidden_size));
-  c.take<int32_t>((size_t)((group_blocks(n_routes, kGroupChunk) + 1) * (g.num_experts + 1)));
+  c.take<int32_t>((size_t)group_hist_rows(group_blocks(n_routes, kGroupChunk)) * (g.num_experts + 1));
   return align_up(c.offset, 256);
 }
 
@@ -704,7 +704,7 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     grp.E = g.num_experts;
     uint16_t* h = c.take<uint16_t>((size_t)(n_routes * g.intermediate_size));
     float* P = c.take<float>((size_t)(n_routes * g.hidden_size));
-    int32_t* hist = c.take<int32_t>((size_t)((group_blocks(n_routes, kGroupChunk) + 1) * (g.num_experts + 1)));
+    int32_t* hist = c.take<int32_t>((size_t)group_hist_rows(group_blocks(n_routes, kGroupChunk)) * (g.num_experts + 1));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts;
     launch_group(expert_ids, n_routes, E, grp, hist, &hdr->status, s);

@@ -1,9 +1,11 @@
 // Stable grouping of routes by expert, in three passes over fixed chunks:
 //   1. a histogram of each chunk's expert ids (hist_kernel here, or fused
 //      into the routing kernel of the prefill path),
-//   2. bases_kernel: per chunk and expert, the routes of that expert in
-//      earlier chunks, and the expert offsets (routes to lower experts),
-//   3. scatter_kernel: each workgroup places its chunk's routes in flat order
+//   2. superblock_sums_kernel: the histograms summed over superblocks of
+//      kSuperChunks chunks (one wave each),
+//   3. scatter_kernel: each workgroup derives its chunk's bucket bases (the
+//      superblock sums before it, the chunks of its superblock before it)
+//      and the expert offsets, then places its chunk's routes in flat order
 //      (ballot-matched ranks within each wave).
 // Reference: MLXNativeGraniteMoEPrefill.h:666-684 (argsort of the flat expert
 // ids and its inverse); the order produced is (expert asc, flat index asc).
@@ -36,103 +38,49 @@ __global__ __launch_bounds__(256) void hist_kernel(const int32_t* __restrict__ i
   if (tid <= E) hist[(int64_t)blockIdx.x * (E + 1) + tid] = h[tid];
 }
 
-// Bucket bases of every chunk from the chunk histograms:
-//   part[c][b] = sum_{c' < c} hist[c'][b]   (b in [0, E])
-// plus offsets (exclusive scan of the bucket totals over the E valid
-// experts), the active list and the status word. One workgroup of W waves:
-// wave w owns a contiguous range of chunks, lane l buckets l and 64 + l.
-// Pass 1 sums each wave's range per bucket, the per-wave sums are scanned
-// over waves, pass 2 walks the range again writing running prefixes. part
-// may alias hist: an entry is read and then written by the same lane.
-constexpr int kBaseThreads = 1024;
-constexpr int kBaseWaves = kBaseThreads / 64;
+// Superblock sums: bsum[sb][b] = sum of hist[c][b] over the kSuperChunks
+// chunks of superblock sb. One wave per superblock, lane l buckets l and
+// 64 + l; all rows are requested before the first is added.
+constexpr int kSuperChunks = 16;
 
-__global__ __launch_bounds__(kBaseThreads) void bases_kernel(const int32_t* hist, int nblocks, int E,
-                                                             int32_t* part, int32_t* __restrict__ offsets,
-                                                             int32_t* __restrict__ active,
-                                                             uint32_t* __restrict__ status) {
-  __shared__ int wsum[kBaseWaves][66];
-  __shared__ int tot[66];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+__global__ __launch_bounds__(64) void superblock_sums_kernel(const int32_t* __restrict__ hist, int nblocks,
+                                                             int E, int32_t* __restrict__ bsum) {
+  const int sb = blockIdx.x;
+  const int lane = threadIdx.x;
   const int B = E + 1;
-  const bool has0 = lane < B, has1 = 64 + lane < B;
-  const int cpw = (nblocks + kBaseWaves - 1) / kBaseWaves;
-  const int c0 = min(nblocks, wave * cpw), c1 = min(nblocks, c0 + cpw);
-  // Rows are read 16 at a time with unconditional loads (indices clamped to
-  // a valid entry, the value then masked), so a wave waits for memory once
-  // per 16 rows rather than once per row.
-  constexpr int kBatch = 16;
-  // Buffer loads: entries outside this wave's rows or buckets get an offset
-  // past the buffer and read as zero.
   const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int32_t*>(hist), (short)0, (int)((uint32_t)nblocks * B * 4), 0x00020000);
-  auto batch = [&](int cb, int (&v0)[kBatch], int (&v1)[kBatch]) {
+  int v0[kSuperChunks], v1[kSuperChunks];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int c = cb + k;
-      const uint32_t row = (uint32_t)c * B * 4;
-      v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (has0 && c < c1) ? row + lane * 4 : 0x80000000u, 0, 0);
-      v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (has1 && c < c1) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
-    }
-  };
+  for (int k = 0; k < kSuperChunks; ++k) {
+    const int c = sb * kSuperChunks + k;
+    const uint32_t row = (uint32_t)c * B * 4;
+    v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < nblocks && lane < B) ? row + lane * 4 : 0x80000000u, 0, 0);
+    v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < nblocks && 64 + lane < B) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
+  }
   int s0 = 0, s1 = 0;
-  for (int cb = c0; cb < c1; cb += kBatch) {
-    int v0[kBatch], v1[kBatch];
-    batch(cb, v0, v1);
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      s0 += v0[k];
-      s1 += v1[k];
-    }
+  for (int k = 0; k < kSuperChunks; ++k) {
+    s0 += v0[k];
+    s1 += v1[k];
   }
-  if (has0) wsum[wave][lane] = s0;
-  if (has1) wsum[wave][64 + lane] = s1;
-  __syncthreads();
-  if (tid < B) {
-    int acc = 0;
-    for (int w = 0; w < kBaseWaves; ++w) {
-      const int v = wsum[w][tid];
-      wsum[w][tid] = acc;
-      acc += v;
-    }
-    tot[tid] = acc;
+  if (lane < B) bsum[(int64_t)sb * B + lane] = s0;
+  if (64 + lane < B) bsum[(int64_t)sb * B + 64 + lane] = s1;
+}
+
+// Grouping of zero routes: offsets all zero, no active expert, status clear.
+__global__ void group_empty_kernel(int E, Grouping g, uint32_t* __restrict__ status) {
+  const int tid = threadIdx.x;
+  if (tid <= E) g.offsets[tid] = 0;
+  if (tid == 0) {
+    g.active[E] = 0;
+    *status = 0u;
   }
-  __syncthreads();
-  if (wave == 0) {
-    const int t = lane < E ? tot[lane] : 0;
-    int incl = t;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
-    const int valid = __shfl(incl, 63, 64);
-    if (lane < E) offsets[lane] = incl - t;
-    if (lane == 0) offsets[E] = valid;
-    const uint64_t act = __ballot(lane < E && t > 0);
-    if (lane < E && t > 0) active[__popcll(act & lanemask_lt())] = lane;
-    if (lane == 0) {
-      active[E] = __popcll(act);
-      *status = tot[E] > 0 ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
-    }
-  }
-  int r0 = has0 ? wsum[wave][lane] : 0, r1 = has1 ? wsum[wave][64 + lane] : 0;
-  for (int cb = c0; cb < c1; cb += kBatch) {
-    int v0[kBatch], v1[kBatch];
-    batch(cb, v0, v1);
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int c = cb + k;
-      if (c < c1) {
-        if (has0) part[(int64_t)c * B + lane] = r0;
-        if (has1) part[(int64_t)c * B + 64 + lane] = r1;
-      }
-      r0 += v0[k];
-      r1 += v1[k];
-    }
-  }
+}
+
+static void launch_group_empty(int E, Grouping g, uint32_t* status, hipStream_t s) {
+  group_empty_kernel<<<1, 128, 0, s>>>(E, g, status);
+  check_hip(hipGetLastError(), "group launch");
 }
 
 // Places the routes of chunk blockIdx.x: position of a route = first position
@@ -140,8 +88,8 @@ __global__ __launch_bounds__(kBaseThreads) void bases_kernel(const int32_t* hist
 // every valid route) + its rank among the chunk's routes of that bucket.
 template <int THREADS>
 __global__ __launch_bounds__(THREADS) void scatter_kernel(
-    const int32_t* __restrict__ ids, int64_t n, int E, int chunk, const int32_t* __restrict__ part,
-    const int32_t* __restrict__ offsets, int32_t* __restrict__ order, int32_t* __restrict__ inverse) {
+    const int32_t* __restrict__ ids, int64_t n, int E, int chunk, const int32_t* __restrict__ hist,
+    const int32_t* __restrict__ bsum, int nblocks, Grouping g, uint32_t* __restrict__ status) {
   __shared__ int base[65];
   __shared__ int run[65];
   __shared__ int wcnt[THREADS / 64][65];
@@ -149,10 +97,79 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
   const int wave = tid >> 6;
   const int b = blockIdx.x;
   const int B = E + 1;
-  for (int i = tid; i < B; i += THREADS) {
-    base[i] = part[(int64_t)b * B + i] + offsets[i < E ? i : E];
-    run[i] = 0;
+  if (tid < 64) {
+    // Bucket bases of this chunk: lane l holds buckets l and 64 + l. The
+    // bucket totals are every superblock's sums; the routes before this chunk
+    // are the superblocks before its own plus its superblock's earlier chunks.
+    const int lane = tid;
+    const int nsb = (nblocks + kSuperChunks - 1) / kSuperChunks;
+    const int sbi = b / kSuperChunks;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(bsum), (short)0, (int)((uint32_t)nsb * B * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(hist), (short)0, (int)((uint32_t)nblocks * B * 4), 0x00020000);
+    int tot0 = 0, tot1 = 0, pre0 = 0, pre1 = 0;
+    constexpr int kBatch = 32;
+    for (int r0 = 0; r0 < nsb; r0 += kBatch) {
+      int v0[kBatch], v1[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int r = r0 + k;
+        const uint32_t row = (uint32_t)r * B * 4;
+        v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, (r < nsb && lane < B) ? row + lane * 4 : 0x80000000u, 0, 0);
+        v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, (r < nsb && 64 + lane < B) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        tot0 += v0[k];
+        tot1 += v1[k];
+        if (r0 + k < sbi) {
+          pre0 += v0[k];
+          pre1 += v1[k];
+        }
+      }
+    }
+    {
+      int v0[kSuperChunks], v1[kSuperChunks];
+#pragma unroll
+      for (int k = 0; k < kSuperChunks; ++k) {
+        const int c = sbi * kSuperChunks + k;
+        const uint32_t row = (uint32_t)c * B * 4;
+        v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < b && lane < B) ? row + lane * 4 : 0x80000000u, 0, 0);
+        v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < b && 64 + lane < B) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < kSuperChunks; ++k) {
+        pre0 += v0[k];
+        pre1 += v1[k];
+      }
+    }
+    // Offsets: exclusive scan of the valid experts' totals.
+    const int t = lane < E ? tot0 : 0;
+    int incl = t;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    const int valid = __shfl(incl, 63, 64);
+    if (lane < E) base[lane] = incl - t + pre0;
+    // The bad-id bucket E starts after every valid route.
+    if (E < 64 && lane == E) base[E] = valid + pre0;
+    if (E == 64 && lane == 0) base[64] = valid + pre1;
+    const int bad_total = E < 64 ? __shfl(tot0, E, 64) : __shfl(tot1, 0, 64);
+    if (b == 0) {
+      if (lane < E) g.offsets[lane] = incl - t;
+      if (lane == 0) g.offsets[E] = valid;
+      const uint64_t act = __ballot(lane < E && t > 0);
+      if (lane < E && t > 0) g.active[__popcll(act & lanemask_lt())] = lane;
+      if (lane == 0) {
+        g.active[E] = __popcll(act);
+        *status = bad_total > 0 ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
+      }
+    }
   }
+  for (int i = tid; i < B; i += THREADS) run[i] = 0;
   for (int i = tid; i < (THREADS / 64) * 65; i += THREADS) (&wcnt[0][0])[i] = 0;
   __syncthreads();
 
@@ -175,8 +192,8 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
     if (live) {
       int pos = base[bk] + run[bk] + rank_w;
       for (int w = 0; w < wave; ++w) pos += wcnt[w][bk];
-      order[pos] = (int32_t)f;
-      inverse[f] = pos;
+      g.order[pos] = (int32_t)f;
+      g.inverse[f] = pos;
     }
     __syncthreads();
     for (int i = tid; i < B; i += THREADS) {
@@ -193,21 +210,29 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
 
 int group_blocks(int64_t n, int chunk) { return (int)((n + chunk - 1) / chunk); }
 
+int group_hist_rows(int64_t nblocks) {
+  return (int)(nblocks + 1 + (nblocks + kSuperChunks - 1) / kSuperChunks + 1);
+}
+
 void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, int32_t* hist,
                           Grouping g, uint32_t* status, hipStream_t s) {
   const int nb = group_blocks(n, chunk);
-  // The chunk bases overwrite the histograms in place.
-  bases_kernel<<<1, kBaseThreads, 0, s>>>(hist, nb, E, hist, g.offsets, g.active, status);
-  check_hip(hipGetLastError(), "group bases launch");
-  if (nb > 0) {
-    // One wave per workgroup for small chunks (the routing kernel's chunks).
-    if (chunk <= 64)
-      scatter_kernel<64><<<nb, 64, 0, s>>>(ids, n, E, chunk, hist, g.offsets, g.order, g.inverse);
-    else
-      scatter_kernel<kScatterThreads><<<nb, kScatterThreads, 0, s>>>(ids, n, E, chunk, hist, g.offsets,
-                                                                    g.order, g.inverse);
-    check_hip(hipGetLastError(), "group scatter launch");
+  if (nb <= 0) {
+    // No routes: empty offsets and active list, clear status.
+    launch_group_empty(E, g, status, s);
+    return;
   }
+  const int nsb = (nb + kSuperChunks - 1) / kSuperChunks;
+  // Superblock sums live after the chunk histograms (group_hist_rows rows).
+  int32_t* bsum = hist + (int64_t)(nb + 1) * (E + 1);
+  superblock_sums_kernel<<<nsb, 64, 0, s>>>(hist, nb, E, bsum);
+  check_hip(hipGetLastError(), "group superblock sums launch");
+  // One wave per workgroup for small chunks (the routing kernel's chunks).
+  if (chunk <= 64)
+    scatter_kernel<64><<<nb, 64, 0, s>>>(ids, n, E, chunk, hist, bsum, nb, g, status);
+  else
+    scatter_kernel<kScatterThreads><<<nb, kScatterThreads, 0, s>>>(ids, n, E, chunk, hist, bsum, nb, g, status);
+  check_hip(hipGetLastError(), "group scatter launch");
 }
 
 void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, int32_t* hist, uint32_t* status,

@@ -71,6 +71,9 @@ void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs,
 constexpr int kGroupChunk = 512;           // routes per chunk for given routes
 constexpr int kTopkTokensPerBlock = 4;     // tokens per routing workgroup (chunk = 4*K)
 int group_blocks(int64_t n, int chunk);
+// Rows of E+1 counts the histogram workspace needs for nblocks chunks (the
+// chunk histograms, then the superblock sums).
+int group_hist_rows(int64_t nblocks);
 void launch_group(const int32_t* ids, int64_t n, int E, Grouping g, int32_t* hist, uint32_t* status,
                   hipStream_t s);
 // Scatter with chunk histograms already built (overwritten by chunk bases).
