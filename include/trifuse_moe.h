@@ -3,7 +3,7 @@
  *
  * The library replaces, for one GPU, the MoE feed-forward path of TriFuse's
  * ExecuTorch MLX overlay: router linear, routing (OLMoE or Granite rules),
- * token-to-expert grouping, MLX affine 4-bit group-64 expert matmuls
+ * token-to-expert grouping, MLX affine 4-bit or 8-bit group-64 expert matmuls
  * (gate/up -> SwiGLU -> down) and the weighted combine (+ residual).
  *
  * Conventions
@@ -16,10 +16,10 @@
  *  - Every entry point returns an int status (TFM_OK == 0). No C++ exception
  *    crosses the ABI; tfm_last_error() returns the calling thread's message.
  *  - Affine weight layout (identical to MLX / TriFuse packs):
- *      Q      uint32 [E, N, Kin/8], 8 nibbles per word, LSB first
+ *      Q      uint32 [E, N, Kin*bits/32], p = 32/bits codes per word, LSB first
  *      scales dtype  [E, N, Kin/group]
  *      biases dtype  [E, N, Kin/group]
- *      w[n,k] = scales[n,k/group] * ((Q[n,k/8] >> 4*(k%8)) & 15) + biases[n,k/group]
+ *      w[n,k] = scales[n,k/group] * ((Q[n,k/p] >> bits*(k%p)) & (2^bits-1)) + biases[n,k/group]
  *    (native_affine_ops.py:29-36). gate/up: N = I, Kin = H; down: N = H, Kin = I.
  *  - Matmuls are "transpose=true": y = x . w^T (native_affine_lowering.py:28-31).
  *  - Plans are immutable once created and may be shared by threads. Calls that
@@ -69,7 +69,7 @@ typedef struct tfm_geometry {
   int32_t num_experts;       /* E: 1..64                                 */
   int32_t experts_per_token; /* K: 1..E                                  */
   int32_t group_size;        /* 64                                       */
-  int32_t bits;              /* 4                                        */
+  int32_t bits;              /* 4 or 8 (8-bit: grouped GEMM path only)   */
   int32_t dtype;             /* TFM_DTYPE_*                              */
   int32_t route;             /* TFM_ROUTE_*                              */
   int32_t router;            /* TFM_ROUTER_*                             */

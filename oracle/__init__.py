@@ -147,12 +147,22 @@ def group(idx, E: int):
     return order, inverse, offsets
 
 
+def _bits(words: int, kin: int) -> int:
+    """Code width implied by a packed row of `words` uint32 holding `kin` codes."""
+    bits = 32 * words // kin
+    if bits not in (4, 8) or bits * kin != 32 * words:
+        raise ValueError(f"{words} words do not pack {kin} codes at 4 or 8 bits")
+    return bits
+
+
 def dequant_f64(q, s, b, group_size: int = 64) -> np.ndarray:
     q, s, b = _u32(q), _u16(s), _u16(b)
     N, W = q.shape
-    Kin = W * 8
+    Kin = s.shape[1] * group_size
+    bits = _bits(W, Kin)
     out = np.empty((N, Kin), dtype=np.float64)
-    load().orc_dequant_f64(_p(q), _p(s), _p(b), c_int(N), c_int(Kin), c_int(group_size), _p(out))
+    load().orc_dequant_f64(_p(q), _p(s), _p(b), c_int(N), c_int(Kin), c_int(group_size),
+                           c_int(bits), _p(out))
     return out
 
 
@@ -160,11 +170,12 @@ def gather_qmm_f64(x, xrow, eid, q, s, b, group_size: int = 64) -> np.ndarray:
     x, q, s, b = _u16(x), _u32(q), _u16(s), _u16(b)
     xrow, eid = _i32(xrow).reshape(-1), _i32(eid).reshape(-1)
     E, N, W = q.shape
-    Kin = W * 8
+    Kin = s.shape[2] * group_size
+    bits = _bits(W, Kin)
     rows = eid.size
     out = np.empty((rows, N), dtype=np.float64)
     load().orc_gather_qmm_f64(_p(x), _p(xrow), _p(eid), c_int(rows), _p(q), _p(s), _p(b),
-                              c_int(N), c_int(Kin), c_int(group_size), _p(out))
+                              c_int(N), c_int(Kin), c_int(group_size), c_int(bits), _p(out))
     return out
 
 
@@ -183,8 +194,9 @@ def moe_reference(x, idx, gates, w, tokens=None, residual=None, rm: float = 1.0)
     args = []
     for proj in ("gate", "up", "down"):
         args += [_u32(getattr(w, proj + "_q")), _u16(getattr(w, proj + "_s")), _u16(getattr(w, proj + "_b"))]
+    bits = _bits(w.gate_q.shape[2], H)
     load().orc_moe_reference(_p(x), _p(res), c_float(rm), _p(tok), c_int(tok.size), c_int(H),
-                             c_int(I), c_int(K), _p(idx), _p(gates), c_int(64),
+                             c_int(I), c_int(K), _p(idx), _p(gates), c_int(64), c_int(bits),
                              *[_p(a) for a in args], _p(out))
     return out
 
@@ -206,8 +218,10 @@ def moe_block_cpu(x, w, route: str, router, router_bias=None, residual=None, rm:
     args = []
     for proj in ("gate", "up", "down"):
         args += [_u32(getattr(w, proj + "_q")), _u16(getattr(w, proj + "_s")), _u16(getattr(w, proj + "_b"))]
+    bits = _bits(w.gate_q.shape[2], H)
     used = load().orc_moe_block_cpu(
         _p(x), _p(res), c_float(rm), c_int(T), c_int(H), c_int(E), c_int(K), c_int(I), c_int(64),
+        c_int(bits),
         c_int(0 if route == "olmoe" else 1), _p(_u16(router)), _p(rb), *[_p(a) for a in args],
         _p(idx), _p(gates), _p(y), c_int(threads))
     return y, idx, gates, used

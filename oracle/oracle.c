@@ -224,11 +224,12 @@ int orc_group(const int32_t* idx, int64_t n, int E,
 }
 
 void orc_dequant_f64(const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                     int N, int Kin, int group, double* w) {
-  const int words = Kin / 8, groups = Kin / group;
+                     int N, int Kin, int group, int bits, double* w) {
+  const int per = 32 / bits, words = Kin / per, groups = Kin / group;
+  const uint32_t mask = (1u << bits) - 1u;
   for (int n = 0; n < N; ++n)
     for (int k = 0; k < Kin; ++k) {
-      const uint32_t code = (q[(int64_t)n * words + k / 8] >> (4 * (k % 8))) & 0xFu;
+      const uint32_t code = (q[(int64_t)n * words + k / per] >> (bits * (k % per))) & mask;
       const double sc = orc_bf16_to_f32(s[(int64_t)n * groups + k / group]);
       const double bi = orc_bf16_to_f32(b[(int64_t)n * groups + k / group]);
       w[(int64_t)n * Kin + k] = sc * (double)code + bi;
@@ -237,15 +238,15 @@ void orc_dequant_f64(const uint32_t* q, const uint16_t* s, const uint16_t* b,
 
 void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* eid,
                         int rows, const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                        int N, int Kin, int group, double* out) {
-  const int64_t qe = (int64_t)N * (Kin / 8), se = (int64_t)N * (Kin / group);
+                        int N, int Kin, int group, int bits, double* out) {
+  const int64_t qe = (int64_t)N * (Kin / (32 / bits)), se = (int64_t)N * (Kin / group);
   double* w = (double*)malloc(sizeof(double) * (size_t)N * (size_t)Kin);
   double* xf = (double*)malloc(sizeof(double) * (size_t)Kin);
   int last = -1;
   for (int r = 0; r < rows; ++r) {
     const int e = eid[r];
     if (e != last) {
-      orc_dequant_f64(q + e * qe, s + e * se, b + e * se, N, Kin, group, w);
+      orc_dequant_f64(q + e * qe, s + e * se, b + e * se, N, Kin, group, bits, w);
       last = e;
     }
     const uint16_t* xr = x + (int64_t)xrow[r] * Kin;
@@ -263,13 +264,14 @@ void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* e
 
 void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
                        const int32_t* tokens, int ntok, int H, int I, int K,
-                       const int32_t* idx, const float* gates, int group,
+                       const int32_t* idx, const float* gates, int group, int bits,
                        const uint32_t* gq, const uint16_t* gs, const uint16_t* gb,
                        const uint32_t* uq, const uint16_t* us, const uint16_t* ub,
                        const uint32_t* dq, const uint16_t* ds, const uint16_t* db,
                        double* out) {
-  const int64_t gu_e = (int64_t)I * (H / 8), gu_s = (int64_t)I * (H / group);
-  const int64_t d_e = (int64_t)H * (I / 8), d_s = (int64_t)H * (I / group);
+  const int per = 32 / bits;
+  const int64_t gu_e = (int64_t)I * (H / per), gu_s = (int64_t)I * (H / group);
+  const int64_t d_e = (int64_t)H * (I / per), d_s = (int64_t)H * (I / group);
   double* wg = (double*)malloc(sizeof(double) * (size_t)I * (size_t)H);
   double* wu = (double*)malloc(sizeof(double) * (size_t)I * (size_t)H);
   double* wd = (double*)malloc(sizeof(double) * (size_t)H * (size_t)I);
@@ -290,9 +292,9 @@ void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
     for (int i = 0; i < ntok && !used; ++i)
       for (int k = 0; k < K; ++k) used |= idx[(int64_t)tokens[i] * K + k] == e;
     if (!used) continue;
-    orc_dequant_f64(gq + e * gu_e, gs + e * gu_s, gb + e * gu_s, I, H, group, wg);
-    orc_dequant_f64(uq + e * gu_e, us + e * gu_s, ub + e * gu_s, I, H, group, wu);
-    orc_dequant_f64(dq + e * d_e, ds + e * d_s, db + e * d_s, H, I, group, wd);
+    orc_dequant_f64(gq + e * gu_e, gs + e * gu_s, gb + e * gu_s, I, H, group, bits, wg);
+    orc_dequant_f64(uq + e * gu_e, us + e * gu_s, ub + e * gu_s, I, H, group, bits, wu);
+    orc_dequant_f64(dq + e * d_e, ds + e * d_s, db + e * d_s, H, I, group, bits, wd);
     for (int i = 0; i < ntok; ++i) {
       const int t = tokens[i];
       for (int k = 0; k < K; ++k) {

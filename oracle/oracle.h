@@ -13,7 +13,8 @@
  * Each function cites the reference file:line it follows.
  *
  * Storage: activations, router weights, scales and biases are bf16 held as
- * uint16_t bit patterns. Packed weights are uint32 words, 8 LSB-first nibbles.
+ * uint16_t bit patterns. Packed weights are uint32 words of 32/bits LSB-first
+ * codes (8 nibbles for 4-bit, 4 bytes for 8-bit).
  */
 #ifndef TFM_ORACLE_H
 #define TFM_ORACLE_H
@@ -84,17 +85,18 @@ void orc_route_granite(const uint16_t* logits, int T, int E, int K,
 int orc_group(const int32_t* idx, int64_t n, int E,
               int32_t* order, int32_t* inverse, int32_t* offsets);
 
-/* Affine dequantisation w = s*q + b of one expert matrix Q[N,Kin/8], S/B
- * [N,Kin/g] to fp64 (exact for bf16 S/B). Reference: native_affine_ops.py:29-36. */
+/* Affine dequantisation w = s*q + b of one expert matrix Q[N,Kin*bits/32]
+ * (32/bits codes per word, LSB first), S/B [N,Kin/g] to fp64 (exact for bf16
+ * S/B). bits is 4 or 8. Reference: native_affine_ops.py:29-36. */
 void orc_dequant_f64(const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                     int N, int Kin, int group, double* w);
+                     int N, int Kin, int group, int bits, double* w);
 
 /* gather_qmm, transpose=true: out[r,n] = sum_k x[xrow[r],k] * W[eid[r]][n,k]
  * in fp64 from exact dequantised weights. Reference: native_affine_ops.py:55-63;
  * MLXNativeGraniteMoEPrefill.h:542-550. */
 void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* eid,
                         int rows, const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                        int N, int Kin, int group, double* out);
+                        int N, int Kin, int group, int bits, double* out);
 
 /* Numeric reference of the MoE block for the listed tokens: fp64 accumulation
  * over exact dequantised weights, SwiGLU in fp64, weighted combine with the
@@ -103,7 +105,7 @@ void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* e
  * Reference: MLXNativeGraniteMoEPrefill.h:627-702 (moe). */
 void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
                        const int32_t* tokens, int ntok, int H, int I, int K,
-                       const int32_t* idx, const float* gates, int group,
+                       const int32_t* idx, const float* gates, int group, int bits,
                        const uint32_t* gq, const uint16_t* gs, const uint16_t* gb,
                        const uint32_t* uq, const uint16_t* us, const uint16_t* ub,
                        const uint32_t* dq, const uint16_t* ds, const uint16_t* db,
@@ -115,7 +117,7 @@ void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
  * router_bias may be NULL. Writes idx/gates (gates as fp32 values) and
  * y [T,H] bf16. Returns the number of threads used. */
 int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
-                      int T, int H, int E, int K, int I, int group, int route_kind,
+                      int T, int H, int E, int K, int I, int group, int bits, int route_kind,
                       const uint16_t* router_w, const float* router_bias,
                       const uint32_t* gq, const uint16_t* gs, const uint16_t* gb,
                       const uint32_t* uq, const uint16_t* us, const uint16_t* ub,

@@ -25,12 +25,14 @@
 static inline float bf(float v) { return orc_bf16_to_f32(orc_f32_to_bf16(v)); }
 
 static void dequant_row(const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                        int Kin, int group, float* w) {
+                        int Kin, int group, int bits, float* w) {
+  const int per = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
   for (int g = 0; g < Kin / group; ++g) {
     const float sc = orc_bf16_to_f32(s[g]), bi = orc_bf16_to_f32(b[g]);
-    for (int k = g * group; k < (g + 1) * group; k += 8) {
-      const uint32_t word = q[k / 8];
-      for (int i = 0; i < 8; ++i) w[k + i] = sc * (float)((word >> (4 * i)) & 0xFu) + bi;
+    for (int k = g * group; k < (g + 1) * group; k += per) {
+      const uint32_t word = q[k / per];
+      for (int i = 0; i < per; ++i) w[k + i] = sc * (float)((word >> (bits * i)) & mask) + bi;
     }
   }
 }
@@ -42,7 +44,7 @@ static inline float dot(const float* a, const float* b, int n) {
 }
 
 int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
-                      int T, int H, int E, int K, int I, int group, int route_kind,
+                      int T, int H, int E, int K, int I, int group, int bits, int route_kind,
                       const uint16_t* router_w, const float* router_bias,
                       const uint32_t* gq, const uint16_t* gs, const uint16_t* gb,
                       const uint32_t* uq, const uint16_t* us, const uint16_t* ub,
@@ -79,8 +81,9 @@ int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
   orc_group(idx, R, E, order, inverse, offsets);
 
   const int nb = 16; /* rows per work item */
-  const int64_t gu_e = (int64_t)I * (H / 8), gu_s = (int64_t)I * (H / group);
-  const int64_t d_e = (int64_t)H * (I / 8), d_s = (int64_t)H * (I / group);
+  const int per = 32 / bits;
+  const int64_t gu_e = (int64_t)I * (H / per), gu_s = (int64_t)I * (H / group);
+  const int64_t d_e = (int64_t)H * (I / per), d_s = (int64_t)H * (I / group);
 #pragma omp parallel
   {
     float* wg = (float*)malloc(sizeof(float) * (size_t)H);
@@ -92,9 +95,9 @@ int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
       for (int n0 = 0; n0 < I; n0 += nb) {
         if (offsets[e] == offsets[e + 1]) continue;
         for (int n = n0; n < n0 + nb && n < I; ++n) {
-          const int64_t qr = e * gu_e + (int64_t)n * (H / 8), sr = e * gu_s + (int64_t)n * (H / group);
-          dequant_row(gq + qr, gs + sr, gb + sr, H, group, wg);
-          dequant_row(uq + qr, us + sr, ub + sr, H, group, wu);
+          const int64_t qr = e * gu_e + (int64_t)n * (H / per), sr = e * gu_s + (int64_t)n * (H / group);
+          dequant_row(gq + qr, gs + sr, gb + sr, H, group, bits, wg);
+          dequant_row(uq + qr, us + sr, ub + sr, H, group, bits, wu);
           for (int j = offsets[e]; j < offsets[e + 1]; ++j) {
             const float* xr = xf + (int64_t)(order[j] / K) * H;
             const float up = bf(dot(xr, wu, H));
@@ -110,8 +113,8 @@ int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
       for (int c0 = 0; c0 < H; c0 += nb) {
         if (offsets[e] == offsets[e + 1]) continue;
         for (int c = c0; c < c0 + nb && c < H; ++c) {
-          const int64_t qr = e * d_e + (int64_t)c * (I / 8), sr = e * d_s + (int64_t)c * (I / group);
-          dequant_row(dq + qr, ds + sr, db + sr, I, group, wd);
+          const int64_t qr = e * d_e + (int64_t)c * (I / per), sr = e * d_s + (int64_t)c * (I / group);
+          dequant_row(dq + qr, ds + sr, db + sr, I, group, bits, wd);
           for (int j = offsets[e]; j < offsets[e + 1]; ++j)
             ybuf[(int64_t)j * H + c] = bf(dot(hbuf + (int64_t)j * I, wd, I));
         }

@@ -54,7 +54,7 @@ def _geom(**kw):
     (dict(num_experts=128, experts_per_token=8), _lib.TFM_E_UNSUPPORTED, "num_experts"),
     (dict(dtype=_lib.TFM_DTYPE_F16), _lib.TFM_E_UNSUPPORTED, "bf16"),
     (dict(router=_lib.TFM_ROUTER_AFFINE), _lib.TFM_E_UNSUPPORTED, "router"),
-    (dict(bits=8), _lib.TFM_E_UNSUPPORTED, "4-bit"),
+    (dict(bits=16), _lib.TFM_E_INVALID, "bits"),
     (dict(group_size=128), _lib.TFM_E_UNSUPPORTED, "group_size 64"),
 ])
 def test_plan_create_rejects(kw, code, msg):

@@ -59,19 +59,22 @@ def test_expf_accuracy_and_special_cases():
 # ---------------------------------------------------------------- affine format
 
 def np_dequant(q, s, b, group=64, msb_first=False):
-    """native_affine_ops.py:29-36 restated: LSB-first nibbles, codes*S + B."""
-    shifts = np.arange(8, dtype=np.uint32) * 4
+    """native_affine_ops.py:29-36 restated: LSB-first codes of width
+    32 * words / Kin, codes*S + B."""
+    per = q.shape[-1] and (s.shape[-1] * group) // q.shape[-1]
+    bits = 32 // per
+    shifts = np.arange(per, dtype=np.uint32) * bits
     if msb_first:
         shifts = shifts[::-1]
-    codes = (q.astype(np.uint32)[..., None] >> shifts) & 0xF
-    codes = codes.reshape(*q.shape[:-1], q.shape[-1] * 8).astype(np.float64)
+    codes = (q.astype(np.uint32)[..., None] >> shifts) & ((1 << bits) - 1)
+    codes = codes.reshape(*q.shape[:-1], q.shape[-1] * per).astype(np.float64)
     return codes * np.repeat(f(s), group, -1) + np.repeat(f(b), group, -1)
 
 
-def rand_affine(E, N, Kin):
-    q = RNG.integers(0, 2 ** 32, size=(E, N, Kin // 8), dtype=np.uint64).astype(np.uint32)
-    s = bf(RNG.uniform(0.005, 0.02, size=(E, N, Kin // 64)))
-    b = bf(-8 * f(s))
+def rand_affine(E, N, Kin, bits=4):
+    q = RNG.integers(0, 2 ** 32, size=(E, N, Kin * bits // 32), dtype=np.uint64).astype(np.uint32)
+    s = bf(RNG.uniform(0.005, 0.02, size=(E, N, Kin // 64)) * (16 / 2 ** bits))
+    b = bf(-(2 ** (bits - 1)) * f(s))
     return q, s, b
 
 
@@ -91,9 +94,37 @@ def test_dequant_closed_form_and_nibble_order():
     np.testing.assert_array_equal(got, (codes - 8) * np.repeat(f(s[0]), 64, -1))
 
 
-def test_gather_qmm_brute_force_tiny():
+def test_dequant_8bit_closed_form_and_byte_order():
+    q, s, b = rand_affine(1, 16, 256, bits=8)
+    assert q.shape == (1, 16, 64)
+    got = oracle.dequant_f64(q[0], s[0], b[0])
+    np.testing.assert_array_equal(got, np_dequant(q[0], s[0], b[0]))
+    # a single word 0x03020100 decodes to codes 0..3 in element order; 0xFF is 255
+    qq = np.zeros((1, 16), np.uint32)
+    qq[0, 0], qq[0, 1] = 0x03020100, 0x00FF7F80
+    one, zero = bf(np.ones((1, 1))), bf(np.zeros((1, 1)))
+    np.testing.assert_array_equal(oracle.dequant_f64(qq, one, zero)[0, :8], [0, 1, 2, 3, 128, 127, 255, 0])
+    # planted mistakes: MSB-first bytes, and reading the words as nibbles
+    assert not np.array_equal(got, np_dequant(q[0], s[0], b[0], msb_first=True))
+    nib = (q[0].astype(np.uint32)[..., None] >> (np.arange(8, dtype=np.uint32) * 4)) & 0xF
+    assert not np.array_equal(got[:, :64], nib.reshape(16, -1)[:, :64] * np.repeat(f(s[0]), 64, -1)[:, :64])
+    # bias = -128 scale makes dequant exact: s * (q - 128)
+    codes = np_dequant(q[0], bf(np.ones_like(f(s[0]))), bf(np.zeros_like(f(s[0]))))
+    assert codes.max() > 15
+    np.testing.assert_array_equal(got, (codes - 128) * np.repeat(f(s[0]), 64, -1))
+
+
+def test_dequant_rejects_inconsistent_width():
+    q = np.zeros((2, 12), np.uint32)  # 12 words for 128 codes: neither 4 nor 8 bits
+    s = bf(np.ones((2, 2)))
+    with pytest.raises(ValueError):
+        oracle.dequant_f64(q, s, s)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_brute_force_tiny(bits):
     E, N, Kin, rows = 3, 8, 128, 11
-    q, s, b = rand_affine(E, N, Kin)
+    q, s, b = rand_affine(E, N, Kin, bits)
     x = bf(RNG.standard_normal((5, Kin)))
     xrow = RNG.integers(0, 5, rows).astype(np.int32)
     eid = RNG.integers(0, E, rows).astype(np.int32)
@@ -261,10 +292,10 @@ class W:
     pass
 
 
-def tiny_block(E=4, H=128, I=64):
+def tiny_block(E=4, H=128, I=64, bits=4):
     w = W()
     for proj, (N, Kin) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
-        q, s, b = rand_affine(E, N, Kin)
+        q, s, b = rand_affine(E, N, Kin, bits)
         setattr(w, proj + "_q", q)
         setattr(w, proj + "_s", s)
         setattr(w, proj + "_b", b)
@@ -293,8 +324,9 @@ def np_block(x, idx, gates, w, residual=None, rm=1.0, swap_gate_up=False):
     return y
 
 
-def test_moe_reference_matches_independent_block():
-    w = tiny_block()
+@pytest.mark.parametrize("bits", [4, 8])
+def test_moe_reference_matches_independent_block(bits):
+    w = tiny_block(bits=bits)
     x = bf(RNG.standard_normal((6, 128)))
     idx = RNG.integers(0, 4, (6, 2)).astype(np.int32)
     gates = RNG.random((6, 2)).astype(np.float32)
@@ -309,10 +341,10 @@ def test_moe_reference_matches_independent_block():
     np.testing.assert_allclose(sub, ref[[4, 1]], rtol=1e-10, atol=1e-10)
 
 
-@pytest.mark.parametrize("route", ["olmoe", "granite"])
-def test_cpu_block_matches_reference(route):
+@pytest.mark.parametrize("route,bits", [("olmoe", 4), ("granite", 4), ("olmoe", 8)])
+def test_cpu_block_matches_reference(route, bits):
     E, H, I, K = 8, 256, 128, 2
-    w = tiny_block(E, H, I)
+    w = tiny_block(E, H, I, bits)
     router = bf(RNG.standard_normal((E, H)) * 0.02)
     x = bf(RNG.standard_normal((40, H)))
     y, idx, gates, used = oracle.moe_block_cpu(x, w, route, router, top_k=K, threads=2)

@@ -105,7 +105,6 @@ static void check_geometry(const tfm_geometry& g) {
   if (g.num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built (wave-wide routing)");
   if (g.dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 activations/scales are built");
   if (g.router != TFM_ROUTER_DENSE) fail(TFM_E_UNSUPPORTED, "only the dense router is built");
-  if (g.bits != 4) fail(TFM_E_UNSUPPORTED, "only 4-bit weights are built");
   if (g.group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
 }
 
@@ -153,8 +152,10 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // The decode path (routing per token, grouping in the gate/up prologue)
 // applies when every route fits one grouping thread and both matmul widths
 // fit one 32-element chunk per lane.
+// The decode kernels read 4-bit weights only; 8-bit weights take the grouped
+// GEMM at every batch size.
 static bool fused_decode(const tfm_geometry& g, int64_t R) {
-  return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
+  return g.bits == 4 && R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
 
 struct GroupWs {
@@ -277,11 +278,11 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     uint16_t* Y = reinterpret_cast<uint16_t*>(ws.P);
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, ws.h, s);
+      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, g.bits, ws.h, s);
     }
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, Y, s);
+      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, g.bits, Y, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
     launch_combine_rows(Y, ws.grp.inverse, ws.grp.offsets + E, gates, (int)T, K, H, residual,
@@ -321,7 +322,7 @@ int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
     tfm_plan* p = new tfm_plan{};
     p->g = *geometry;
     p->device = dev;
-    p->gemv_max_routes = gemv_threshold();
+    p->gemv_max_routes = geometry->bits == 4 ? gemv_threshold() : -1;
     *plan_out = p;
   });
 }
@@ -454,7 +455,7 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     need(group_size == 32 || group_size == 64 || group_size == 128, "group_size must be 32, 64 or 128");
     need(k_in % group_size == 0, "k_in must be a multiple of group_size");
     if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
-    if (bits != 4 || group_size != 64) fail(TFM_E_UNSUPPORTED, "only 4-bit group-64 weights are built");
+    if (group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
     if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
     if (n_out % 64 != 0) fail(TFM_E_UNSUPPORTED, "n_out must be a multiple of 64");
     GroupWs ws = carve_group(rows, num_experts, workspace);
@@ -471,12 +472,12 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
     const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
     const int max_active = (int)(rows < num_experts ? rows : num_experts);
-    if (rows <= gemv_threshold() && k_in <= 2048)
+    if (bits == 4 && rows <= gemv_threshold() && k_in <= 2048)
       launch_gemv_plain(static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
                         static_cast<uint16_t*>(out), s);
     else
       launch_ggemm_plain(static_cast<const uint16_t*>(x), rm, ws.grp, rows, num_experts, *w, n_out,
-                         k_in, static_cast<uint16_t*>(out), s);
+                         k_in, bits, static_cast<uint16_t*>(out), s);
   });
 }
 
@@ -716,8 +717,9 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
       launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
       launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
     } else {
-      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, h, s);
-      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, static_cast<uint16_t*>(out_sorted), s);
+      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, g.bits, h, s);
+      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, g.bits,
+                        static_cast<uint16_t*>(out_sorted), s);
     }
   });
 }

@@ -7,8 +7,9 @@
 //   * copies BM activation rows (x rows of the routed tokens, or rows of the
 //     expert-sorted SwiGLU output) from global memory straight into LDS
 //     (buffer loads with an LDS destination),
-//   * loads BN packed 4-bit weight rows into registers, dequantises them
-//     (s*q+b in fp32, rounded to bf16) and writes them to LDS,
+//   * loads BN packed weight rows (4-bit: 32 bytes, 8-bit: 64 bytes of each
+//     row per step) into registers, dequantises them (s*q+b in fp32,
+//     rounded to bf16) and writes them to LDS,
 //   * runs v_mfma_f32_32x32x16_bf16 on the two LDS tiles, each wave owning a
 //     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane).
 //
@@ -66,7 +67,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gg_rsrc(const void* base, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// 8 nibbles (one 32-bit word of a weight row) -> 8 bf16 (s*q+b).
+// 4 bytes (one 32-bit word of an 8-bit weight row) -> 4 bf16 (s*q+b).
+__device__ __forceinline__ uint2 dequant_word_u8(uint32_t w, float s, float b) {
+  float d[4];
+  dequant4_u8(w, s, b, d);
+  uint2 pk;
+  pk.x = pack_bf16x2(d[0], d[1]);
+  pk.y = pack_bf16x2(d[2], d[3]);
+  return pk;
+}
+
+// 8 nibbles (one 32-bit word of a 4-bit weight row) -> 8 bf16 (s*q+b).
 __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
   float d[8];
   dequant8(w, s, b, d);
@@ -95,21 +106,24 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* ds
 #endif
 }
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS_>
 struct GgCfg {
-  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, BITS = BITS_;
+  static constexpr int CPR_B = BITS / 2;            // 16-byte packed chunks of a weight row per step
   static constexpr int WAVES = WAVES_M * WAVES_N;
   static constexpr int THREADS = WAVES * 64;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int MB = WM / 32;                // 32-row MFMA blocks per wave
   static constexpr int NB = WN / 32;                // 32-column MFMA blocks per wave
   static constexpr int LA = BM / (8 * WAVES);       // 8-row LDS copies per wave per step
-  static constexpr int LB = BN * 2 / THREADS;       // packed 16-byte chunks per thread per step
+  static constexpr int LB = BN * CPR_B / THREADS;   // packed 16-byte chunks per thread per step
   static constexpr int OUT_COLS = MODE == kGgGateUp ? BN / 2 : BN;
   static constexpr int WCOLS = MODE == kGgGateUp ? WN / 2 : WN;   // output columns per wave
   static constexpr int SROW = WCOLS + 8;            // staging row stride (bf16), 16 B pad
   static_assert(LA >= 1 && LA * 8 * WAVES == BM, "A copies must tile the block rows");
-  static_assert(LB >= 1 && LB * THREADS == BN * 2, "B chunks must tile the block columns");
+  static_assert(BITS == 4 || BITS == 8, "4-bit or 8-bit weights");
+  static_assert(LB >= 1 && LB * THREADS == BN * CPR_B, "B chunks must tile the block columns");
+  static_assert(64 % CPR_B == 0 && (64 / CPR_B) <= BN / 2, "a wave's chunks stay in one half of the tile");
   static_assert(LB * 4 >= 3, "B words are spread over three sub-steps");
   static_assert(MODE != kGgGateUp || NB % 2 == 0, "gate/up wave tiles pair gate and up blocks");
   static_assert(WAVES % 4 == 0, "staging blocks are spread over the four LDS stages");
@@ -123,9 +137,10 @@ struct RawB {
   uint32_t s[LB], bias[LB];
 };
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS>
 __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgArgs args) {
-  using C = GgCfg<BM_, BN_, WAVES_M_, WAVES_N_, MODE>;
+  using C = GgCfg<BM_, BN_, WAVES_M_, WAVES_N_, MODE, BITS>;
+  constexpr int CPR_B = C::CPR_B;
   constexpr int BM = C::BM, BN = C::BN, MB = C::MB, NB = C::NB, LA = C::LA, LB = C::LB;
   constexpr int T = C::THREADS;
   // Two stages each of A and B, as separate objects so that the compiler's
@@ -204,42 +219,50 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   };
 
   // ---- B: packed weights ----
-  // Chunk q = i*T + tid -> weight row q/2, half q%2 (32 nibbles). Gate/up
-  // tiles hold BN/2 gate rows then BN/2 up rows.
-  const uint32_t qrow = (uint32_t)args.Kin / 2, srow = (uint32_t)(args.Kin / BK) * 2;
+  // Chunk q = i*T + tid -> weight row q/CPR_B, part q%CPR_B (16 bytes: 32
+  // nibbles or 16 bytes of codes). Gate/up tiles hold BN/2 gate rows then
+  // BN/2 up rows.
+  const uint32_t qrow = (uint32_t)args.Kin * BITS / 8, srow = (uint32_t)(args.Kin / BK) * 2;
   __amdgpu_buffer_rsrc_t rbq[LB], rbs[LB], rbb[LB];
   uint32_t b_qoff[LB], b_soff[LB];
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
     const int qw = i * T + wave * 64;  // first chunk of this wave (uniform)
-    const bool up = MODE == kGgGateUp && (qw >> 1) >= BN / 2;
+    const bool up = MODE == kGgGateUp && qw / CPR_B >= BN / 2;
     const tfm_affine& bm = up ? args.wb : args.wa;
     const int q = qw + lane;
-    const int r = q >> 1;
+    const int r = q / CPR_B;
     const int bn = MODE == kGgGateUp ? n0 + (r & (BN / 2 - 1)) : n0 + r;
     const size_t ebase = (size_t)e * args.N;
     rbq[i] = gg_rsrc(reinterpret_cast<const char*>(bm.q) + ebase * qrow, (uint32_t)args.N * qrow);
     rbs[i] = gg_rsrc(static_cast<const char*>(bm.scales) + ebase * srow, (uint32_t)args.N * srow);
     rbb[i] = gg_rsrc(static_cast<const char*>(bm.biases) + ebase * srow, (uint32_t)args.N * srow);
     const bool ok = bn < args.N;
-    b_qoff[i] = ok ? (uint32_t)bn * qrow + (q & 1) * 16 : kOob;
+    b_qoff[i] = ok ? (uint32_t)bn * qrow + (q % CPR_B) * 16 : kOob;
     b_soff[i] = ok ? (uint32_t)bn * srow : kOob;
   }
   auto bload = [&](RawB<LB>& st, int kt) {
     const bool live = kt < KT;
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
-      st.b[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[i] : rnull, b_qoff[i], kt * 32, 0));
+      st.b[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[i] : rnull, b_qoff[i], kt * (BK * BITS / 8), 0));
       st.s[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbs[i] : rnull, b_soff[i], kt * 2, 0);
       st.bias[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbb[i] : rnull, b_soff[i], kt * 2, 0);
     }
   };
-  // Word w (of LB*4) of the dequantised B step.
+  // Word w (of LB*4) of the dequantised B step: 8 elements (one LDS chunk)
+  // for 4-bit, 4 elements (half a chunk) for 8-bit.
   auto bstore_word = [&](const RawB<LB>& st, uint16_t* dst, int w) {
     const int i = w / 4, k = w % 4;
     const int q = i * T + tid;
-    const uint4 pk = dequant_word(word_of(st.b[i], k), bf2f((uint16_t)st.s[i]), bf2f((uint16_t)st.bias[i]));
-    *reinterpret_cast<uint4*>(&dst[swz(q >> 1, (q & 1) * 4 + k)]) = pk;
+    const float sc = bf2f((uint16_t)st.s[i]), bi = bf2f((uint16_t)st.bias[i]);
+    if constexpr (BITS == 4) {
+      const uint4 pk = dequant_word(word_of(st.b[i], k), sc, bi);
+      *reinterpret_cast<uint4*>(&dst[swz(q >> 1, (q & 1) * 4 + k)]) = pk;
+    } else {
+      const uint2 pk = dequant_word_u8(word_of(st.b[i], k), sc, bi);
+      *reinterpret_cast<uint2*>(&dst[swz(q >> 2, (q & 3) * 2 + (k >> 1)) + (k & 1) * 4]) = pk;
+    }
   };
 
   // ---- wave tile ----
@@ -398,63 +421,73 @@ static unsigned grid_for(int64_t n_routes, int E, int BM, int NT) {
   return (unsigned)total;
 }
 
-template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE>
+template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE, int BITS>
 static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
-  using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE>;
+  using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS>;
   const int NT = (a.N + C::OUT_COLS - 1) / C::OUT_COLS;
-  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE><<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS><<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+}
+
+template <int MODE, int BITS>
+static void launch_tile(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  if (use_tall(n_routes, E))
+    launch_one<256, 256, 2, 4, MODE, BITS>(a, n_routes, E, s);
+  else
+    launch_one<128, 256, 2, 4, MODE, BITS>(a, n_routes, E, s);
 }
 
 template <int MODE>
-static void launch_mode(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
-  if (use_tall(n_routes, E))
-    launch_one<256, 256, 2, 4, MODE>(a, n_routes, E, s);
+static void launch_mode(const GgArgs& a, int bits, int64_t n_routes, int E, hipStream_t s) {
+  if (bits == 8)
+    launch_tile<MODE, 8>(a, n_routes, E, s);
   else
-    launch_one<128, 256, 2, 4, MODE>(a, n_routes, E, s);
+    launch_tile<MODE, 4>(a, n_routes, E, s);
 }
 
-static void check_shapes(int N, int Kin, int64_t x_rows) {
+static void check_shapes(int N, int Kin, int bits, int64_t x_rows) {
+  if (bits != 4 && bits != 8) fail(TFM_E_UNSUPPORTED, "grouped GEMM: weights must be 4-bit or 8-bit");
   if (Kin % BK != 0) fail(TFM_E_UNSUPPORTED, "grouped GEMM: input width must be a multiple of 64");
   if (N % 64 != 0) fail(TFM_E_UNSUPPORTED, "grouped GEMM: output width must be a multiple of 64");
   // Buffer offsets are 32-bit: activations and one expert's packed weights
   // must stay below 2 GiB.
-  if ((double)x_rows * Kin * 2 >= 2147483648.0 || (double)N * Kin / 2 >= 2147483648.0)
+  if ((double)x_rows * Kin * 2 >= 2147483648.0 || (double)N * Kin * bits / 8 >= 2147483648.0)
     fail(TFM_E_UNSUPPORTED, "grouped GEMM: operand of 2 GiB or more");
 }
 
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         uint16_t* h, hipStream_t s) {
+                         int bits, uint16_t* h, hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin, rm.nx);
+  check_shapes(N, Kin, bits, rm.nx);
   GgArgs a{};
   a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = gate; a.wb = up;
   a.N = N; a.Kin = Kin; a.out = h;
-  launch_mode<kGgGateUp>(a, n_routes, E, s);
+  launch_mode<kGgGateUp>(a, bits, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM gate/up launch");
 }
 
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, uint16_t* y_sorted, hipStream_t s) {
+                       const tfm_affine& w, int N, int Kin, int bits, uint16_t* y_sorted,
+                       hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin, n_routes);
+  check_shapes(N, Kin, bits, n_routes);
   GgArgs a{};
   a.x = hsorted; a.x_bytes = (uint32_t)(n_routes * Kin * 2);
   a.rm = RowMap{g.order, nullptr, 1, 0, nullptr}; a.g = g; a.wa = w; a.wb = w; a.N = N;
   a.Kin = Kin; a.out = y_sorted;
-  launch_mode<kGgDown>(a, n_routes, E, s);
+  launch_mode<kGgDown>(a, bits, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM down launch");
 }
 
 void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
-                        int E, const tfm_affine& w, int N, int Kin, uint16_t* out,
+                        int E, const tfm_affine& w, int N, int Kin, int bits, uint16_t* out,
                         hipStream_t s) {
   if (n_routes <= 0) return;
-  check_shapes(N, Kin, rm.nx);
+  check_shapes(N, Kin, bits, rm.nx);
   GgArgs a{};
   a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = w; a.wb = w;
   a.N = N; a.Kin = Kin; a.out = out;
-  launch_mode<kGgPlain>(a, n_routes, E, s);
+  launch_mode<kGgPlain>(a, bits, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM plain launch");
 }
 

@@ -120,6 +120,15 @@ __device__ __forceinline__ void dequant8(uint32_t w, float s, float b, float* ou
   out[7] = __builtin_fmaf(s, (float)(hi >> 24), b);
 }
 
+// 4 bytes (one 32-bit word of an 8-bit weight row, LSB first) -> 4 values
+// s*q+b; each byte converts with one v_cvt_f32_ubyteN.
+__device__ __forceinline__ void dequant4_u8(uint32_t w, float s, float b, float* out) {
+  out[0] = __builtin_fmaf(s, (float)(w & 0xffu), b);
+  out[1] = __builtin_fmaf(s, (float)((w >> 8) & 0xffu), b);
+  out[2] = __builtin_fmaf(s, (float)((w >> 16) & 0xffu), b);
+  out[3] = __builtin_fmaf(s, (float)(w >> 24), b);
+}
+
 // Sum_i q_i * x_i over the 8 nibbles of a packed word (x in element order).
 __device__ __forceinline__ float qdot8(uint32_t w, const float* x, float acc) {
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;

@@ -169,11 +169,12 @@ void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_acti
 //   plain:  out[order[j], :] = bf16(x W^T)                 (gather_qmm)
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         uint16_t* h, hipStream_t s);
+                         int bits, uint16_t* h, hipStream_t s);
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, uint16_t* y_sorted, hipStream_t s);
+                       const tfm_affine& w, int N, int Kin, int bits, uint16_t* y_sorted,
+                       hipStream_t s);
 void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
-                        int E, const tfm_affine& w, int N, int Kin, uint16_t* out,
+                        int E, const tfm_affine& w, int N, int Kin, int bits, uint16_t* out,
                         hipStream_t s);
 
 // Combine of gate-weighted fp32 rows (decode path):

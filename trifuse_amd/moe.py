@@ -278,6 +278,7 @@ class MoEBlock:
         self.experts_per_token = experts_per_token
         self.route_kind = route
         self.residual_multiplier = residual_multiplier
+        self.bits = bits
         self.geometry = Geometry(hidden_size, intermediate_size, num_experts, experts_per_token,
                                  group_size, bits, TFM_DTYPE_BF16, _ROUTES[route], TFM_ROUTER_DENSE,
                                  float(residual_multiplier))
@@ -350,19 +351,19 @@ class MoEBlock:
 
     def _build_weights(self, w: ExpertWeights, router: bool) -> MoeWeights:
         H, I, E = self.hidden_size, self.intermediate_size, self.num_experts
-        g = 64
+        g, per = 64, 32 // self.bits
         shapes = {
-            "gate_q": (E, I, H // 8), "gate_s": (E, I, H // g), "gate_b": (E, I, H // g),
-            "up_q": (E, I, H // 8), "up_s": (E, I, H // g), "up_b": (E, I, H // g),
-            "down_q": (E, H, I // 8), "down_s": (E, H, I // g), "down_b": (E, H, I // g),
+            "gate_q": (E, I, H // per), "gate_s": (E, I, H // g), "gate_b": (E, I, H // g),
+            "up_q": (E, I, H // per), "up_s": (E, I, H // g), "up_b": (E, I, H // g),
+            "down_q": (E, H, I // per), "down_s": (E, H, I // g), "down_b": (E, H, I // g),
         }
         for name, shape in shapes.items():
             t = getattr(w, name)
             if tuple(t.shape) != shape:
                 raise ValueError(f"{name} shape {tuple(t.shape)} != {shape}")
-        validate_affine(w.gate_q, w.gate_s, w.gate_b, 64, 4, 3)
-        validate_affine(w.up_q, w.up_s, w.up_b, 64, 4, 3)
-        validate_affine(w.down_q, w.down_s, w.down_b, 64, 4, 3)
+        validate_affine(w.gate_q, w.gate_s, w.gate_b, 64, self.bits, 3)
+        validate_affine(w.up_q, w.up_s, w.up_b, 64, self.bits, 3)
+        validate_affine(w.down_q, w.down_s, w.down_b, 64, self.bits, 3)
         for name in ("gate_s", "up_s", "down_s"):
             _check_bf16(getattr(w, name), name)
         mw = MoeWeights()

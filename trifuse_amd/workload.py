@@ -12,7 +12,9 @@ the same bytes can be produced on the host and on the GPU:
 Distributions (per tensor):
   router  W_r [E, H] bf16 ~ N(0, 0.02)
   Q       [E, N, Kin/8] uint32 (stored as int32), 8 uniform nibbles per word
+          (8-bit layers: [E, N, Kin/4], 4 uniform bytes per word)
   scales  [E, N, Kin/64] bf16 ~ U[0.005, 0.02];  biases = -8 * scales (exact)
+          (8-bit layers: U[0.005, 0.02] / 16, biases = -128 * scales)
   x       [T, H] bf16 ~ N(0, 1)
   Zipf router bias (skewed routing): bias_e = 0.875 * (-1.1 * ln r_e) with r
   a seeded permutation of 1..E, added to the fp32 router logits.
@@ -162,16 +164,23 @@ class LayerWeights:
 
 
 def make_layer(geom: Geometry, layer: int, device="cpu", zipf: bool = False,
-               seed_tag: str = "") -> LayerWeights:
+               seed_tag: str = "", bits: int = 4) -> LayerWeights:
+    """Synthetic layer. Codes are uniform over [0, 2^bits) and the bias is
+    -2^(bits-1) * scale, so weights are centred on zero; 8-bit scales are
+    1/16 of the 4-bit ones, which keeps the weight range the same."""
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
     E, H, I = geom.experts, geom.hidden, geom.intermediate
-    tag = (geom.name, seed_tag, layer)
+    tag = (geom.name, seed_tag, layer) if bits == 4 else (geom.name, seed_tag, layer, bits)
     w = {}
     w["router"] = normal_bf16((E, H), 0.02, _key(*tag, "router")).to(device)
+    shrink = 16.0 / (1 << bits)
     for proj, (N, Kin) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
-        w[f"{proj}_q"] = packed_nibbles((E, N, Kin // 8), _key(*tag, proj, "q"), device)
-        s = uniform_scales((E, N, Kin // GROUP), _key(*tag, proj, "s"), device)
+        w[f"{proj}_q"] = packed_nibbles((E, N, Kin * bits // 32), _key(*tag, proj, "q"), device)
+        s = uniform_scales((E, N, Kin // GROUP), _key(*tag, proj, "s"), device,
+                           lo=0.005 * shrink, hi=0.02 * shrink)
         w[f"{proj}_s"] = s
-        w[f"{proj}_b"] = (s.float() * -8.0).to(torch.bfloat16)
+        w[f"{proj}_b"] = (s.float() * -float(1 << (bits - 1))).to(torch.bfloat16)
     lb = zipf_bias(E, _key(*tag, "zipf")).to(device) if zipf else None
     return LayerWeights(logit_bias=lb, **w)
 
