@@ -44,14 +44,16 @@ extern "C" {
 #define TFM_E_DEVICE 5      /* device-side check failed (see tfm_status_word) */
 
 /* ---- enums ----------------------------------------------------------- */
-#define TFM_DTYPE_BF16 0 /* graded activation/scale dtype                 */
-#define TFM_DTYPE_F16 1  /* TriFuse's shipped packs (not built yet)       */
+#define TFM_DTYPE_BF16 0 /* activations, scales and biases in bf16         */
+#define TFM_DTYPE_F16 1  /* IEEE half: TriFuse's shipped packs; needs the
+                            affine router, runs the grouped GEMM at every
+                            batch size                                    */
 
 #define TFM_ROUTE_OLMOE 0   /* softmax over E, top-K probabilities         */
 #define TFM_ROUTE_GRANITE 1 /* top-K logits, softmax over the K selected   */
 
 #define TFM_ROUTER_DENSE 0  /* router weight dtype [E,H]                   */
-#define TFM_ROUTER_AFFINE 1 /* affine-quantised router (not built yet)     */
+#define TFM_ROUTER_AFFINE 1 /* affine-quantised router (group 64)          */
 
 /* tfm_moe_forward / tfm_moe_experts flags */
 #define TFM_FLAG_DETERMINISTIC 1u /* accepted for compatibility: every path reduces the K routes of a token in k order */
@@ -93,11 +95,17 @@ typedef struct tfm_affine {
 } tfm_affine;
 
 typedef struct tfm_moe_weights {
-  const void* router;       /* dense router weight [E, H] in dtype         */
+  const void* router;       /* TFM_ROUTER_DENSE: router weight [E, H] in dtype */
   const float* logit_bias;  /* optional [E] fp32 added to the router logits
                                before rounding; no counterpart in the
                                reference (synthetic routing skew). NULL = none */
   tfm_affine gate, up, down;
+  /* TFM_ROUTER_AFFINE: the router as an affine-quantised [E, H] matrix
+   * (Q [E, H*router_bits/32], S/B [E, H/64] in dtype), the `mlp.gate` /
+   * `router.layer` Affine of export_native_olmoe_target.py:160-171,194-200 and
+   * export_native_granite_target.py:231-237. Logits are rounded to dtype. */
+  tfm_affine router_affine;
+  int32_t router_bits;      /* 4 or 8 (TFM_ROUTER_AFFINE only)             */
 } tfm_moe_weights;
 
 /* ---- routing --------------------------------------------------------- */
@@ -106,11 +114,23 @@ typedef struct tfm_moe_weights {
  *   x       [T, H] dtype
  *   logits  optional out [T, E] dtype (NULL = not returned)
  *   idx     out [T, K] int32, slot order of the reference
- *   gates   out [T, K]: dtype for OLMoE (bf16 probabilities), fp32 for Granite */
+ *   gates   out [T, K]: dtype for OLMoE (probabilities), fp32 for Granite
+ * Needs a TFM_ROUTER_DENSE plan with bf16 dtype. */
 int tfm_route(const tfm_plan* plan, const void* x, int64_t tokens,
               const void* router, const float* logit_bias, void* logits,
               int32_t* idx, void* gates, void* workspace, size_t workspace_bytes,
               void* stream);
+
+/* tfm_route for a TFM_ROUTER_AFFINE plan: the router linear is the
+ * affine-quantised matmul of the exports' router module
+ * (`torch.ops.mlx.native_affine_qmm(x, W, S, B, 64, bits)`,
+ * export_native_olmoe_target.py:166-167,200; export_native_granite_target.py:236-237).
+ * router: Q [E, H*router_bits/32], S/B [E, H/64] in dtype. Logits are
+ * tree-reduced like the dense router's over w = dtype(s*q + b). */
+int tfm_route_affine(const tfm_plan* plan, const void* x, int64_t tokens,
+                     const tfm_affine* router, int32_t router_bits, const float* logit_bias,
+                     void* logits, int32_t* idx, void* gates, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* Routing from given logits [T, E] (dtype). OLMoE: native_olmoe_softmax +
  * native_olmoe_topk_indices + native_take_along_last

@@ -82,6 +82,34 @@ def f32_to_bf16(f) -> np.ndarray:
     return out
 
 
+_DT = {"bf16": 0, "f16": 1}
+
+
+def _dt(dtype: str) -> c_int:
+    if dtype not in _DT:
+        raise ValueError(f"storage dtype must be 'bf16' or 'f16', not {dtype!r}")
+    return c_int(_DT[dtype])
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = _u16(h)
+    out = np.empty(h.shape, dtype=np.float32)
+    load().orc_f16_to_f32_array(_p(h), _p(out), c_int64(h.size))
+    return out
+
+
+def f32_to_f16(f) -> np.ndarray:
+    f = np.ascontiguousarray(np.asarray(f, dtype=np.float32))
+    out = np.empty(f.shape, dtype=np.uint16)
+    load().orc_f32_to_f16_array(_p(f), _p(out), c_int64(f.size))
+    return out
+
+
+def st_to_f32(h, dtype: str = "bf16") -> np.ndarray:
+    """Storage bits (bf16 or f16) to float32."""
+    return f16_to_f32(h) if _DT[dtype] else bf16_to_f32(h)
+
+
 def expf(x) -> np.ndarray:
     x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
     out = np.empty_like(x)
@@ -99,38 +127,51 @@ def router_logits(x, w, bias=None) -> np.ndarray:
     return out
 
 
-def rmsnorm(x, w, eps: float) -> np.ndarray:
-    """Post-attention RMSNorm (bf16 in and out), bit-defined order (oracle.h)."""
+def router_logits_affine(x, q, s, b, bias=None, dtype: str = "bf16") -> np.ndarray:
+    """Logits of the affine-quantised router Q [E, H*bits/32], S/B [E, H/64]."""
+    x, q, s, b = _u16(x), _u32(q), _u16(s), _u16(b)
+    T, H = x.shape
+    E = q.shape[0]
+    bits = _bits(q.shape[1], H)
+    bb = None if bias is None else np.ascontiguousarray(np.asarray(bias, dtype=np.float32))
+    out = np.empty((T, E), dtype=np.uint16)
+    load().orc_router_logits_affine(_p(x), _p(q), _p(s), _p(b), c_int(bits), _p(bb), c_int(T),
+                                    c_int(H), c_int(E), _dt(dtype), _p(out))
+    return out
+
+
+def rmsnorm(x, w, eps: float, dtype: str = "bf16") -> np.ndarray:
+    """Post-attention RMSNorm (storage dtype in and out), bit-defined order (oracle.h)."""
     x, w = _u16(x), _u16(w)
     T, H = x.shape
     out = np.empty((T, H), dtype=np.uint16)
-    load().orc_rmsnorm(_p(x), _p(w), c_float(eps), c_int(T), c_int(H), _p(out))
+    load().orc_rmsnorm(_p(x), _p(w), c_float(eps), c_int(T), c_int(H), _dt(dtype), _p(out))
     return out
 
 
-def olmoe_softmax(logits) -> np.ndarray:
+def olmoe_softmax(logits, dtype: str = "bf16") -> np.ndarray:
     lg = _u16(logits)
     T, E = lg.shape
     out = np.empty_like(lg)
-    load().orc_olmoe_softmax(_p(lg), c_int(T), c_int(E), _p(out))
+    load().orc_olmoe_softmax(_p(lg), c_int(T), c_int(E), _dt(dtype), _p(out))
     return out
 
 
-def route_olmoe(logits, K: int):
+def route_olmoe(logits, K: int, dtype: str = "bf16"):
     lg = _u16(logits)
     T, E = lg.shape
     idx = np.empty((T, K), dtype=np.int32)
     gates = np.empty((T, K), dtype=np.uint16)
-    load().orc_route_olmoe(_p(lg), c_int(T), c_int(E), c_int(K), _p(idx), _p(gates))
+    load().orc_route_olmoe(_p(lg), c_int(T), c_int(E), c_int(K), _dt(dtype), _p(idx), _p(gates))
     return idx, gates
 
 
-def route_granite(logits, K: int):
+def route_granite(logits, K: int, dtype: str = "bf16"):
     lg = _u16(logits)
     T, E = lg.shape
     idx = np.empty((T, K), dtype=np.int32)
     gates = np.empty((T, K), dtype=np.float32)
-    load().orc_route_granite(_p(lg), c_int(T), c_int(E), c_int(K), _p(idx), _p(gates))
+    load().orc_route_granite(_p(lg), c_int(T), c_int(E), c_int(K), _dt(dtype), _p(idx), _p(gates))
     return idx, gates
 
 
@@ -155,18 +196,18 @@ def _bits(words: int, kin: int) -> int:
     return bits
 
 
-def dequant_f64(q, s, b, group_size: int = 64) -> np.ndarray:
+def dequant_f64(q, s, b, group_size: int = 64, dtype: str = "bf16") -> np.ndarray:
     q, s, b = _u32(q), _u16(s), _u16(b)
     N, W = q.shape
     Kin = s.shape[1] * group_size
     bits = _bits(W, Kin)
     out = np.empty((N, Kin), dtype=np.float64)
     load().orc_dequant_f64(_p(q), _p(s), _p(b), c_int(N), c_int(Kin), c_int(group_size),
-                           c_int(bits), _p(out))
+                           c_int(bits), _dt(dtype), _p(out))
     return out
 
 
-def gather_qmm_f64(x, xrow, eid, q, s, b, group_size: int = 64) -> np.ndarray:
+def gather_qmm_f64(x, xrow, eid, q, s, b, group_size: int = 64, dtype: str = "bf16") -> np.ndarray:
     x, q, s, b = _u16(x), _u32(q), _u16(s), _u16(b)
     xrow, eid = _i32(xrow).reshape(-1), _i32(eid).reshape(-1)
     E, N, W = q.shape
@@ -175,11 +216,12 @@ def gather_qmm_f64(x, xrow, eid, q, s, b, group_size: int = 64) -> np.ndarray:
     rows = eid.size
     out = np.empty((rows, N), dtype=np.float64)
     load().orc_gather_qmm_f64(_p(x), _p(xrow), _p(eid), c_int(rows), _p(q), _p(s), _p(b),
-                              c_int(N), c_int(Kin), c_int(group_size), c_int(bits), _p(out))
+                              c_int(N), c_int(Kin), c_int(group_size), c_int(bits), _dt(dtype), _p(out))
     return out
 
 
-def moe_reference(x, idx, gates, w, tokens=None, residual=None, rm: float = 1.0) -> np.ndarray:
+def moe_reference(x, idx, gates, w, tokens=None, residual=None, rm: float = 1.0,
+                  dtype: str = "bf16") -> np.ndarray:
     """fp64 block output for `tokens` (default all): residual + rm * sum_k g_k expert_k(x).
     `w` has attributes gate_q/gate_s/gate_b/up_*/down_* as numpy arrays."""
     x = _u16(x)
@@ -196,7 +238,7 @@ def moe_reference(x, idx, gates, w, tokens=None, residual=None, rm: float = 1.0)
         args += [_u32(getattr(w, proj + "_q")), _u16(getattr(w, proj + "_s")), _u16(getattr(w, proj + "_b"))]
     bits = _bits(w.gate_q.shape[2], H)
     load().orc_moe_reference(_p(x), _p(res), c_float(rm), _p(tok), c_int(tok.size), c_int(H),
-                             c_int(I), c_int(K), _p(idx), _p(gates), c_int(64), c_int(bits),
+                             c_int(I), c_int(K), _p(idx), _p(gates), c_int(64), c_int(bits), _dt(dtype),
                              *[_p(a) for a in args], _p(out))
     return out
 

@@ -29,6 +29,48 @@ uint16_t orc_f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+/* IEEE half: exact widening; narrowing rounds to nearest even with subnormal
+ * results, overflow to infinity (|f| >= 65520) and quiet NaN. */
+float orc_f16_to_f32(uint16_t h) {
+  const int e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  float v;
+  if (e == 0x1f) v = m ? NAN : INFINITY;
+  else if (e == 0) v = ldexpf((float)m, -24);
+  else v = ldexpf((float)(m | 0x400), e - 25);
+  return (h & 0x8000) ? -v : v;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a >= 0x38800000u) {
+    const uint32_t r = a - 0x38000000u;
+    return (uint16_t)(sign | ((r + 0xfffu + ((r >> 13) & 1u)) >> 13));
+  }
+  if (a <= 0x33000000u) return (uint16_t)sign;
+  const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+  const int sh = 126 - (int)(a >> 23);
+  uint32_t q = m >> sh;
+  const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+  return (uint16_t)(sign | q);
+}
+
+/* Storage dtype dt: 0 = bf16, 1 = IEEE half. */
+static inline float st2f(int dt, uint16_t h) { return dt ? orc_f16_to_f32(h) : orc_bf16_to_f32(h); }
+static inline uint16_t f2st(int dt, float f) { return dt ? orc_f32_to_f16(f) : orc_f32_to_bf16(f); }
+
+void orc_f16_to_f32_array(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32(in[i]);
+}
+
+void orc_f32_to_f16_array(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16(in[i]);
+}
+
 void orc_bf16_to_f32_array(const uint16_t* in, float* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = orc_bf16_to_f32(in[i]);
 }
@@ -92,7 +134,38 @@ void orc_router_logits(const uint16_t* x, const uint16_t* w, const float* bias,
   }
 }
 
-void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out) {
+/* Affine-quantised router: the dense router's order over
+ * w = st(fmaf(s, q, b)) (group 64), x, s, b and logits in storage dtype dt. */
+void orc_router_logits_affine(const uint16_t* x, const uint32_t* q, const uint16_t* s,
+                              const uint16_t* b, int bits, const float* bias, int T, int H, int E,
+                              int dt, uint16_t* logits) {
+  const int c = H / 64, per = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  float* w = (float*)malloc(sizeof(float) * (size_t)H);
+  float lane[64];
+  for (int e = 0; e < E; ++e) {
+    const uint32_t* qr = q + (int64_t)e * (H / per);
+    for (int k = 0; k < H; ++k) {
+      const uint32_t code = (qr[k / per] >> (bits * (k % per))) & mask;
+      const int64_t g = (int64_t)e * (H / 64) + k / 64;
+      w[k] = st2f(dt, f2st(dt, fmaf(st2f(dt, s[g]), (float)code, st2f(dt, b[g]))));
+    }
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* xr = x + (int64_t)t * H;
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < c; ++j) acc = fmaf(st2f(dt, xr[l * c + j]), w[l * c + j], acc);
+        lane[l] = acc;
+      }
+      float v = tree64(lane);
+      if (bias) v = v + bias[e];
+      logits[(int64_t)t * E + e] = f2st(dt, v);
+    }
+  }
+  free(w);
+}
+
+void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, int dt, uint16_t* out) {
   const int c = H / 64;
   float lane[64];
   for (int t = 0; t < T; ++t) {
@@ -100,7 +173,7 @@ void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, 
     for (int l = 0; l < 64; ++l) {
       float s = 0.0f;
       for (int j = 0; j < c; ++j) {
-        const float v = orc_bf16_to_f32(xr[l * c + j]);
+        const float v = st2f(dt, xr[l * c + j]);
         s = fmaf(v, v, s);
       }
       lane[l] = s;
@@ -108,8 +181,8 @@ void orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, 
     const float mean = tree64(lane) / (float)H;
     const float inv = 1.0f / sqrtf(mean + eps);
     for (int h = 0; h < H; ++h) {
-      const float nx = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(xr[h]) * inv));
-      out[(int64_t)t * H + h] = orc_f32_to_bf16(orc_bf16_to_f32(w[h]) * nx);
+      const float nx = st2f(dt, f2st(dt, st2f(dt, xr[h]) * inv));
+      out[(int64_t)t * H + h] = f2st(dt, st2f(dt, w[h]) * nx);
     }
   }
 }
@@ -137,30 +210,30 @@ static void softmax_exps(const float* ld, float* ex) {
   for (int i = 0; i < 64; ++i) ex[i] = orc_expf(ld[i] - maxval);
 }
 
-static void olmoe_probs(const uint16_t* row, int E, uint16_t* p) {
+static void olmoe_probs(const uint16_t* row, int E, int dt, uint16_t* p) {
   float ld[64], ex[64];
-  for (int i = 0; i < 64; ++i) ld[i] = i < E ? orc_bf16_to_f32(row[i]) : -INFINITY;
+  for (int i = 0; i < 64; ++i) ld[i] = i < E ? st2f(dt, row[i]) : -INFINITY;
   softmax_exps(ld, ex);
   const float norm = softmax_normaliser(ex);
-  for (int i = 0; i < E; ++i) p[i] = orc_f32_to_bf16(ex[i] * norm);
+  for (int i = 0; i < E; ++i) p[i] = f2st(dt, ex[i] * norm);
 }
 
-void orc_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs) {
-  for (int t = 0; t < T; ++t) olmoe_probs(logits + (int64_t)t * E, E, probs + (int64_t)t * E);
+void orc_olmoe_softmax(const uint16_t* logits, int T, int E, int dt, uint16_t* probs) {
+  for (int t = 0; t < T; ++t) olmoe_probs(logits + (int64_t)t * E, E, dt, probs + (int64_t)t * E);
 }
 
-void orc_route_olmoe(const uint16_t* logits, int T, int E, int K,
+void orc_route_olmoe(const uint16_t* logits, int T, int E, int K, int dt,
                      int32_t* idx, uint16_t* gates) {
   uint16_t p[64];
   for (int t = 0; t < T; ++t) {
-    olmoe_probs(logits + (int64_t)t * E, E, p);
+    olmoe_probs(logits + (int64_t)t * E, E, dt, p);
     /* MLXOLMoERouter.h:65-83: stable descending rank, NaN last. */
     for (int i = 0; i < E; ++i) {
-      const float v = orc_bf16_to_f32(p[i]);
+      const float v = st2f(dt, p[i]);
       const int vn = v != v;
       int rank = 0;
       for (int j = 0; j < E; ++j) {
-        const float o = orc_bf16_to_f32(p[j]);
+        const float o = st2f(dt, p[j]);
         const int on = o != o;
         const int before = !on && (vn || o > v);
         const int equal = (on && vn) || (!on && !vn && o == v);
@@ -174,12 +247,12 @@ void orc_route_olmoe(const uint16_t* logits, int T, int E, int K,
   }
 }
 
-void orc_route_granite(const uint16_t* logits, int T, int E, int K,
+void orc_route_granite(const uint16_t* logits, int T, int E, int K, int dt,
                        int32_t* idx, float* gates) {
   float v[64], sel[64], ld[64], ex[64];
   for (int t = 0; t < T; ++t) {
     const uint16_t* row = logits + (int64_t)t * E;
-    for (int i = 0; i < E; ++i) v[i] = orc_bf16_to_f32(row[i]);
+    for (int i = 0; i < E; ++i) v[i] = st2f(dt, row[i]);
     /* MLXNativeGraniteMoEPrefill.h:92-109: stable ascending rank, NaN last,
      * the top K ranks land in slots rank-(E-K). */
     for (int i = 0; i < E; ++i) {
@@ -224,21 +297,21 @@ int orc_group(const int32_t* idx, int64_t n, int E,
 }
 
 void orc_dequant_f64(const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                     int N, int Kin, int group, int bits, double* w) {
+                     int N, int Kin, int group, int bits, int dt, double* w) {
   const int per = 32 / bits, words = Kin / per, groups = Kin / group;
   const uint32_t mask = (1u << bits) - 1u;
   for (int n = 0; n < N; ++n)
     for (int k = 0; k < Kin; ++k) {
       const uint32_t code = (q[(int64_t)n * words + k / per] >> (bits * (k % per))) & mask;
-      const double sc = orc_bf16_to_f32(s[(int64_t)n * groups + k / group]);
-      const double bi = orc_bf16_to_f32(b[(int64_t)n * groups + k / group]);
+      const double sc = st2f(dt, s[(int64_t)n * groups + k / group]);
+      const double bi = st2f(dt, b[(int64_t)n * groups + k / group]);
       w[(int64_t)n * Kin + k] = sc * (double)code + bi;
     }
 }
 
 void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* eid,
                         int rows, const uint32_t* q, const uint16_t* s, const uint16_t* b,
-                        int N, int Kin, int group, int bits, double* out) {
+                        int N, int Kin, int group, int bits, int dt, double* out) {
   const int64_t qe = (int64_t)N * (Kin / (32 / bits)), se = (int64_t)N * (Kin / group);
   double* w = (double*)malloc(sizeof(double) * (size_t)N * (size_t)Kin);
   double* xf = (double*)malloc(sizeof(double) * (size_t)Kin);
@@ -246,11 +319,11 @@ void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* e
   for (int r = 0; r < rows; ++r) {
     const int e = eid[r];
     if (e != last) {
-      orc_dequant_f64(q + e * qe, s + e * se, b + e * se, N, Kin, group, bits, w);
+      orc_dequant_f64(q + e * qe, s + e * se, b + e * se, N, Kin, group, bits, dt, w);
       last = e;
     }
     const uint16_t* xr = x + (int64_t)xrow[r] * Kin;
-    for (int k = 0; k < Kin; ++k) xf[k] = orc_bf16_to_f32(xr[k]);
+    for (int k = 0; k < Kin; ++k) xf[k] = st2f(dt, xr[k]);
     for (int n = 0; n < N; ++n) {
       double acc = 0.0;
       const double* wr = w + (int64_t)n * Kin;
@@ -264,7 +337,7 @@ void orc_gather_qmm_f64(const uint16_t* x, const int32_t* xrow, const int32_t* e
 
 void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
                        const int32_t* tokens, int ntok, int H, int I, int K,
-                       const int32_t* idx, const float* gates, int group, int bits,
+                       const int32_t* idx, const float* gates, int group, int bits, int dt,
                        const uint32_t* gq, const uint16_t* gs, const uint16_t* gb,
                        const uint32_t* uq, const uint16_t* us, const uint16_t* ub,
                        const uint32_t* dq, const uint16_t* ds, const uint16_t* db,
@@ -292,14 +365,14 @@ void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
     for (int i = 0; i < ntok && !used; ++i)
       for (int k = 0; k < K; ++k) used |= idx[(int64_t)tokens[i] * K + k] == e;
     if (!used) continue;
-    orc_dequant_f64(gq + e * gu_e, gs + e * gu_s, gb + e * gu_s, I, H, group, bits, wg);
-    orc_dequant_f64(uq + e * gu_e, us + e * gu_s, ub + e * gu_s, I, H, group, bits, wu);
-    orc_dequant_f64(dq + e * d_e, ds + e * d_s, db + e * d_s, H, I, group, bits, wd);
+    orc_dequant_f64(gq + e * gu_e, gs + e * gu_s, gb + e * gu_s, I, H, group, bits, dt, wg);
+    orc_dequant_f64(uq + e * gu_e, us + e * gu_s, ub + e * gu_s, I, H, group, bits, dt, wu);
+    orc_dequant_f64(dq + e * d_e, ds + e * d_s, db + e * d_s, H, I, group, bits, dt, wd);
     for (int i = 0; i < ntok; ++i) {
       const int t = tokens[i];
       for (int k = 0; k < K; ++k) {
         if (idx[(int64_t)t * K + k] != e) continue;
-        for (int c = 0; c < H; ++c) xf[c] = orc_bf16_to_f32(x[(int64_t)t * H + c]);
+        for (int c = 0; c < H; ++c) xf[c] = st2f(dt, x[(int64_t)t * H + c]);
         for (int n = 0; n < I; ++n) {
           double ag = 0.0, au = 0.0;
           const double* rg = wg + (int64_t)n * H;
@@ -327,7 +400,7 @@ void orc_moe_reference(const uint16_t* x, const uint16_t* residual, float rm,
     }
     for (int c = 0; c < H; ++c) {
       o[c] *= (double)rm;
-      if (residual) o[c] += orc_bf16_to_f32(residual[(int64_t)t * H + c]);
+      if (residual) o[c] += st2f(dt, residual[(int64_t)t * H + c]);
     }
   }
   free(contrib); free(wg); free(wu); free(wd); free(xf); free(h);

@@ -71,10 +71,10 @@ int orc_moe_block_cpu(const uint16_t* x, const uint16_t* residual, float rm,
       for (int c = 0; c < H; ++c) xf[(int64_t)t * H + c] = orc_bf16_to_f32(x[(int64_t)t * H + c]);
       if (route_kind == 0) {
         uint16_t g16[64];
-        orc_route_olmoe(logits + (int64_t)t * E, 1, E, K, idx + (int64_t)t * K, g16);
+        orc_route_olmoe(logits + (int64_t)t * E, 1, E, K, 0, idx + (int64_t)t * K, g16);
         for (int k = 0; k < K; ++k) gates[(int64_t)t * K + k] = orc_bf16_to_f32(g16[k]);
       } else {
-        orc_route_granite(logits + (int64_t)t * E, 1, E, K, idx + (int64_t)t * K, gates + (int64_t)t * K);
+        orc_route_granite(logits + (int64_t)t * E, 1, E, K, 0, idx + (int64_t)t * K, gates + (int64_t)t * K);
       }
     }
   }

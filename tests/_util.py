@@ -40,8 +40,12 @@ def np_layer(layer) -> types.SimpleNamespace:
         setattr(ns, proj + "_q", u32(getattr(layer, proj + "_q")))
         setattr(ns, proj + "_s", u16(getattr(layer, proj + "_s")))
         setattr(ns, proj + "_b", u16(getattr(layer, proj + "_b")))
-    ns.router = u16(layer.router)
+    ns.router = None if layer.router is None else u16(layer.router)
     ns.logit_bias = None if layer.logit_bias is None else f32(layer.logit_bias)
+    if getattr(layer, "router_q", None) is not None:
+        ns.router_q = u32(layer.router_q)
+        ns.router_s = u16(layer.router_s)
+        ns.router_b = u16(layer.router_b)
     return ns
 
 

@@ -52,8 +52,9 @@ def _geom(**kw):
     (dict(bits=3), _lib.TFM_E_INVALID, "bits"),
     (dict(group_size=48), _lib.TFM_E_INVALID, "group_size"),
     (dict(num_experts=128, experts_per_token=8), _lib.TFM_E_UNSUPPORTED, "num_experts"),
-    (dict(dtype=_lib.TFM_DTYPE_F16), _lib.TFM_E_UNSUPPORTED, "bf16"),
-    (dict(router=_lib.TFM_ROUTER_AFFINE), _lib.TFM_E_UNSUPPORTED, "router"),
+    (dict(dtype=_lib.TFM_DTYPE_F16), _lib.TFM_E_UNSUPPORTED, "affine router"),
+    (dict(dtype=7), _lib.TFM_E_INVALID, "dtype"),
+    (dict(router=7), _lib.TFM_E_INVALID, "router"),
     (dict(bits=16), _lib.TFM_E_INVALID, "bits"),
     (dict(group_size=128), _lib.TFM_E_UNSUPPORTED, "group_size 64"),
 ])
@@ -75,7 +76,10 @@ def test_null_arguments():
     assert lib.tfm_group(None, 4, 8, None, None, None, None, 0, None) == _lib.TFM_E_INVALID
     assert lib.tfm_topk(None, 4, 65, 8, 0, 0, None, None) == _lib.TFM_E_UNSUPPORTED
     assert lib.tfm_topk(None, 4, 8, 9, 0, 0, None, None) == _lib.TFM_E_INVALID
-    assert lib.tfm_olmoe_softmax(None, 4, 64, _lib.TFM_DTYPE_F16, None, None) == _lib.TFM_E_UNSUPPORTED
+    assert lib.tfm_olmoe_softmax(None, 4, 64, 7, None, None) == _lib.TFM_E_INVALID
+    assert lib.tfm_olmoe_softmax(None, 4, 64, _lib.TFM_DTYPE_F16, None, None) == _lib.TFM_E_INVALID
+    assert b"logits" in lib.tfm_last_error()
+    assert lib.tfm_route_affine(None, None, 4, None, 4, None, None, None, None, None, 0, None) == _lib.TFM_E_INVALID
     assert lib.tfm_profiler_stage(None, 0, None, None, None) == _lib.TFM_E_INVALID
     assert lib.tfm_profiler_create(0, ctypes.byref(ctypes.c_void_p())) == _lib.TFM_E_INVALID
 

@@ -83,6 +83,8 @@ class MoeWeights(ctypes.Structure):
         ("gate", Affine),
         ("up", Affine),
         ("down", Affine),
+        ("router_affine", Affine),
+        ("router_bits", c_int32),
     ]
 
 
@@ -93,6 +95,8 @@ SIGNATURES = {
     "tfm_workspace_bytes": (c_size_t, [c_void_p, c_int64]),
     "tfm_route": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tfm_route_affine": (c_int, [c_void_p, c_void_p, c_int64, POINTER(Affine), c_int32, c_void_p,
+                                 c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tfm_route_logits": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "tfm_olmoe_softmax": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]),
     "tfm_topk": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p]),

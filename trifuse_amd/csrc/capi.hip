@@ -103,8 +103,8 @@ static void check_geometry(const tfm_geometry& g) {
   need(g.group_size == 32 || g.group_size == 64 || g.group_size == 128,
        "group_size must be 32, 64 or 128");
   if (g.num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built (wave-wide routing)");
-  if (g.dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 activations/scales are built");
-  if (g.router != TFM_ROUTER_DENSE) fail(TFM_E_UNSUPPORTED, "only the dense router is built");
+  if (g.dtype == TFM_DTYPE_F16 && g.router != TFM_ROUTER_AFFINE)
+    fail(TFM_E_UNSUPPORTED, "f16 blocks need the affine router (a dense f16 router is not built)");
   if (g.group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
 }
 
@@ -152,10 +152,12 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // The decode path (routing per token, grouping in the gate/up prologue)
 // applies when every route fits one grouping thread and both matmul widths
 // fit one 32-element chunk per lane.
-// The decode kernels read 4-bit weights only; 8-bit weights take the grouped
-// GEMM at every batch size.
+// The decode kernels read 4-bit weights, bf16 activations and the dense
+// router only; other blocks route like prefill, and 8-bit or f16 blocks run
+// the grouped GEMM at every batch size.
 static bool fused_decode(const tfm_geometry& g, int64_t R) {
-  return g.bits == 4 && R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
+  return g.bits == 4 && g.dtype == TFM_DTYPE_BF16 && g.router == TFM_ROUTER_DENSE && R <= 256 &&
+         g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
 
 struct GroupWs {
@@ -225,6 +227,7 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const tfm_geometry& g = p->g;
   const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
   const int64_t R = T * K;
+  const bool f16 = g.dtype == TFM_DTYPE_F16;
   const bool gemv = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
   if (!grouped && gemv && decode_stream_fits((int)T, K, E, H, I)) {
     // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
@@ -278,23 +281,26 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     uint16_t* Y = reinterpret_cast<uint16_t*>(ws.P);
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, g.bits, ws.h, s);
+      launch_ggemm_gateup(x, rm, ws.grp, R, E, w->gate, w->up, I, H, g.bits, f16, ws.h, s);
     }
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, g.bits, Y, s);
+      launch_ggemm_down(ws.h, ws.grp, R, E, w->down, H, I, g.bits, f16, Y, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
-    launch_combine_rows(Y, ws.grp.inverse, ws.grp.offsets + E, gates, (int)T, K, H, residual,
+    launch_combine_rows(f16, Y, ws.grp.inverse, ws.grp.offsets + E, gates, (int)T, K, H, residual,
                         g.residual_multiplier, y, s);
   }
 }
 
-static void check_weights(const tfm_moe_weights* w, bool router) {
+static void check_weights(const tfm_moe_weights* w, bool router, const tfm_geometry& g) {
   need_ptr(w, "weights");
-  if (router) {
+  if (router && g.router == TFM_ROUTER_DENSE) {
     need_ptr(w->router, "weights->router");
     need_align16(w->router, "weights->router");
+  } else if (router) {
+    need(w->router_bits == 4 || w->router_bits == 8, "weights->router_bits must be 4 or 8");
+    check_affine(w->router_affine, "weights->router_affine");
   }
   check_affine(w->gate, "weights->gate");
   check_affine(w->up, "weights->up");
@@ -322,7 +328,7 @@ int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
     tfm_plan* p = new tfm_plan{};
     p->g = *geometry;
     p->device = dev;
-    p->gemv_max_routes = geometry->bits == 4 ? gemv_threshold() : -1;
+    p->gemv_max_routes = geometry->bits == 4 && geometry->dtype == TFM_DTYPE_BF16 ? gemv_threshold() : -1;
     *plan_out = p;
   });
 }
@@ -352,13 +358,42 @@ int tfm_route(const tfm_plan* plan, const void* x, int64_t tokens, const void* r
     need_align16(x, "x");
     need_align16(router, "router");
     const tfm_geometry& g = plan->g;
+    if (g.router != TFM_ROUTER_DENSE || g.dtype != TFM_DTYPE_BF16)
+      fail(TFM_E_UNSUPPORTED, "tfm_route needs a dense-router bf16 plan (use tfm_route_affine)");
     BlockWs ws = carve_block(g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : ws.logits;
     launch_router_logits(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router),
                          logit_bias, (int)tokens, g.hidden_size, g.num_experts, lg, s);
-    launch_topk(g.route, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates, nullptr, s);
+    launch_topk(g.route, false, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates,
+                nullptr, s);
+  });
+}
+
+int tfm_route_affine(const tfm_plan* plan, const void* x, int64_t tokens, const tfm_affine* router,
+                     int32_t router_bits, const float* logit_bias, void* logits, int32_t* idx,
+                     void* gates, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    const tfm_geometry& g = plan->g;
+    if (g.router != TFM_ROUTER_AFFINE) fail(TFM_E_INVALID, "tfm_route_affine needs an affine-router plan");
+    need(router_bits == 4 || router_bits == 8, "router_bits must be 4 or 8");
+    if (tokens == 0) return;
+    need_ptr(x, "x");
+    need_ptr(router, "router");
+    need_ptr(idx, "idx");
+    need_align16(x, "x");
+    check_affine(*router, "router");
+    BlockWs ws = carve_block(g, tokens, workspace);
+    need_ws(workspace, workspace_bytes, ws.bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool f16 = g.dtype == TFM_DTYPE_F16;
+    uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : ws.logits;
+    launch_affine_router_logits(f16, router_bits, static_cast<const uint16_t*>(x), *router, logit_bias,
+                                (int)tokens, g.hidden_size, g.num_experts, lg, s);
+    launch_topk(g.route, f16, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates, nullptr, s);
   });
 }
 
@@ -371,7 +406,7 @@ int tfm_route_logits(const tfm_plan* plan, const void* logits, int64_t tokens, i
     need_ptr(logits, "logits");
     need_ptr(idx, "idx");
     const tfm_geometry& g = plan->g;
-    launch_topk(g.route, static_cast<const uint16_t*>(logits), (int)tokens, g.num_experts,
+    launch_topk(g.route, g.dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(logits), (int)tokens, g.num_experts,
                 g.experts_per_token, idx, gates, nullptr, static_cast<hipStream_t>(stream));
   });
 }
@@ -383,11 +418,11 @@ int tfm_topk(const void* values, int64_t tokens, int32_t n, int32_t k, int32_t r
     need(n > 0 && k > 0 && k <= n, "need 0 < k <= n");
     need(rule == TFM_ROUTE_OLMOE || rule == TFM_ROUTE_GRANITE, "unknown top-k rule");
     if (n > 64) fail(TFM_E_UNSUPPORTED, "top-k over more than 64 values is not built");
-    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    need(dtype == TFM_DTYPE_BF16 || dtype == TFM_DTYPE_F16, "unknown dtype");
     if (tokens == 0) return;
     need_ptr(values, "values");
     need_ptr(idx, "idx");
-    launch_rank_topk(rule, static_cast<const uint16_t*>(values), (int)tokens, n, k, idx,
+    launch_rank_topk(rule, dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(values), (int)tokens, n, k, idx,
                      static_cast<hipStream_t>(stream));
   });
 }
@@ -398,11 +433,11 @@ int tfm_olmoe_softmax(const void* logits, int64_t tokens, int32_t num_experts, i
     need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
     need(num_experts > 0, "num_experts must be positive");
     if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
-    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    need(dtype == TFM_DTYPE_BF16 || dtype == TFM_DTYPE_F16, "unknown dtype");
     if (tokens == 0) return;
     need_ptr(logits, "logits");
     need_ptr(probs, "probs");
-    launch_olmoe_softmax(static_cast<const uint16_t*>(logits), (int)tokens, num_experts,
+    launch_olmoe_softmax(dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(logits), (int)tokens, num_experts,
                          static_cast<uint16_t*>(probs), static_cast<hipStream_t>(stream));
   });
 }
@@ -456,7 +491,7 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     need(k_in % group_size == 0, "k_in must be a multiple of group_size");
     if (num_experts > 64) fail(TFM_E_UNSUPPORTED, "num_experts > 64 is not built");
     if (group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
-    if (dtype != TFM_DTYPE_BF16) fail(TFM_E_UNSUPPORTED, "only bf16 is built");
+    need(dtype == TFM_DTYPE_BF16 || dtype == TFM_DTYPE_F16, "unknown dtype");
     if (n_out % 64 != 0) fail(TFM_E_UNSUPPORTED, "n_out must be a multiple of 64");
     GroupWs ws = carve_group(rows, num_experts, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
@@ -472,12 +507,12 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
     const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
     const int max_active = (int)(rows < num_experts ? rows : num_experts);
-    if (bits == 4 && rows <= gemv_threshold() && k_in <= 2048)
+    if (bits == 4 && dtype == TFM_DTYPE_BF16 && rows <= gemv_threshold() && k_in <= 2048)
       launch_gemv_plain(static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
                         static_cast<uint16_t*>(out), s);
     else
       launch_ggemm_plain(static_cast<const uint16_t*>(x), rm, ws.grp, rows, num_experts, *w, n_out,
-                         k_in, bits, static_cast<uint16_t*>(out), s);
+                         k_in, bits, dtype == TFM_DTYPE_F16, static_cast<uint16_t*>(out), s);
   });
 }
 
@@ -495,7 +530,7 @@ int tfm_moe_experts(const tfm_plan* plan, const void* x, int64_t tokens, const v
     need_align16(x, "x");
     need_align16(y, "y");
     if (residual) need_align16(residual, "residual");
-    check_weights(weights, false);
+    check_weights(weights, false, plan->g);
     BlockWs ws = carve_block(plan->g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     run_experts(plan, static_cast<const uint16_t*>(x), tokens, static_cast<const uint16_t*>(residual),
@@ -583,23 +618,29 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
                                    reinterpret_cast<int32_t*>(gates_out), R, s);
     return;
   }
-  bool fused_route;
+  const bool f16 = g.dtype == TFM_DTYPE_F16;
+  bool fused_route = false;
   {
-    // Router linear, top-k and chunk histograms in one kernel where the
-    // hidden size has a variant; otherwise logits then top-k.
+    // Dense router: router linear, top-k and chunk histograms in one kernel
+    // where the hidden size has a variant; otherwise logits then top-k.
     StageScope st(TFM_STAGE_ROUTER, s);
-    fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
-                                     static_cast<const uint16_t*>(weights->router),
-                                     weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
-                                     ws.hist, nullptr, s);
-    if (!fused_route)
-      launch_router_logits(static_cast<const uint16_t*>(x),
-                           static_cast<const uint16_t*>(weights->router), weights->logit_bias,
-                           (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+    if (g.router == TFM_ROUTER_AFFINE) {
+      launch_affine_router_logits(f16, weights->router_bits, static_cast<const uint16_t*>(x),
+                                  weights->router_affine, weights->logit_bias, T, H, E, ws.logits, s);
+    } else {
+      fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
+                                       static_cast<const uint16_t*>(weights->router),
+                                       weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
+                                       ws.hist, nullptr, s);
+      if (!fused_route)
+        launch_router_logits(static_cast<const uint16_t*>(x),
+                             static_cast<const uint16_t*>(weights->router), weights->logit_bias,
+                             (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+    }
   }
   if (!fused_route) {
     StageScope st(TFM_STAGE_TOPK, s);
-    launch_topk_hist(g.route, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
+    launch_topk_hist(g.route, f16, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
   }
   {
     StageScope st(TFM_STAGE_GROUP, s);
@@ -624,7 +665,7 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
     need_align16(x, "x");
     need_align16(y, "y");
     if (residual) need_align16(residual, "residual");
-    check_weights(weights, true);
+    check_weights(weights, true, plan->g);
     BlockWs ws = carve_block(plan->g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     moe_forward_body(plan, x, tokens, residual, weights, y, idx_out, gates_out, flags, ws,
@@ -648,13 +689,13 @@ int tfm_moe_forward_rmsnorm(const tfm_plan* plan, const void* h, int64_t tokens,
     need_align16(norm_weight, "norm_weight");
     need_align16(y, "y");
     need(y != h, "y must not alias h (h is the residual)");
-    check_weights(weights, true);
+    check_weights(weights, true, plan->g);
     BlockWs ws = carve_block(plan->g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
     {
       StageScope st(TFM_STAGE_NORM, s);
-      launch_rmsnorm(static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(norm_weight), eps,
+      launch_rmsnorm(plan->g.dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(norm_weight), eps,
                      (int)tokens, plan->g.hidden_size, ws.xn, s);
     }
     moe_forward_body(plan, ws.xn, tokens, h, weights, y, idx_out, gates_out, flags, ws, s);
@@ -694,7 +735,7 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     need_ptr(out_sorted, "out_sorted");
     need_ptr(inverse, "inverse");
     need_align16(x, "x");
-    check_weights(weights, false);
+    check_weights(weights, false, plan->g);
     Carver c(workspace);
     WsHeader* hdr = c.take<WsHeader>(1);
     Grouping grp{};
@@ -717,8 +758,9 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
       launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
       launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
     } else {
-      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, g.bits, h, s);
-      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, g.bits,
+      const bool f16 = g.dtype == TFM_DTYPE_F16;
+      launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, g.bits, f16, h, s);
+      launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, g.bits, f16,
                         static_cast<uint16_t*>(out_sorted), s);
     }
   });

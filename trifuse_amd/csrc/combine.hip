@@ -90,9 +90,11 @@ void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t
   check_hip(hipGetLastError(), "combine launch");
 }
 
-// 8 columns per thread; H % 8 == 0. Y rows are bf16 expert outputs (the
+// 8 columns per thread; H % 8 == 0. Y rows are expert outputs in the storage
+// dtype (bf16, or half when F16; the
 // reference's per-route gather_qmm output, MLXNativeGraniteMoEPrefill.h:684),
 // weighted by the fp32 gate and summed in k order.
+template <bool F16>
 __global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ inverse,
                                                            const int32_t* __restrict__ n_valid,
@@ -114,41 +116,44 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __res
     if (row >= nv) continue;
     const float gw = gates[f];
     const uint4 a = *reinterpret_cast<const uint4*>(Y + row * H + c);
-    s[0] = __builtin_fmaf(gw, lo_bf(a.x), s[0]);
-    s[1] = __builtin_fmaf(gw, hi_bf(a.x), s[1]);
-    s[2] = __builtin_fmaf(gw, lo_bf(a.y), s[2]);
-    s[3] = __builtin_fmaf(gw, hi_bf(a.y), s[3]);
-    s[4] = __builtin_fmaf(gw, lo_bf(a.z), s[4]);
-    s[5] = __builtin_fmaf(gw, hi_bf(a.z), s[5]);
-    s[6] = __builtin_fmaf(gw, lo_bf(a.w), s[6]);
-    s[7] = __builtin_fmaf(gw, hi_bf(a.w), s[7]);
+    s[0] = __builtin_fmaf(gw, lo_st<F16>(a.x), s[0]);
+    s[1] = __builtin_fmaf(gw, hi_st<F16>(a.x), s[1]);
+    s[2] = __builtin_fmaf(gw, lo_st<F16>(a.y), s[2]);
+    s[3] = __builtin_fmaf(gw, hi_st<F16>(a.y), s[3]);
+    s[4] = __builtin_fmaf(gw, lo_st<F16>(a.z), s[4]);
+    s[5] = __builtin_fmaf(gw, hi_st<F16>(a.z), s[5]);
+    s[6] = __builtin_fmaf(gw, lo_st<F16>(a.w), s[6]);
+    s[7] = __builtin_fmaf(gw, hi_st<F16>(a.w), s[7]);
   }
   float r[8];
   if (residual) {
     const uint4 rv = *reinterpret_cast<const uint4*>(residual + (int64_t)t * H + c);
-    r[0] = lo_bf(rv.x); r[1] = hi_bf(rv.x); r[2] = lo_bf(rv.y); r[3] = hi_bf(rv.y);
-    r[4] = lo_bf(rv.z); r[5] = hi_bf(rv.z); r[6] = lo_bf(rv.w); r[7] = hi_bf(rv.w);
+    r[0] = lo_st<F16>(rv.x); r[1] = hi_st<F16>(rv.x); r[2] = lo_st<F16>(rv.y); r[3] = hi_st<F16>(rv.y);
+    r[4] = lo_st<F16>(rv.z); r[5] = hi_st<F16>(rv.z); r[6] = lo_st<F16>(rv.w); r[7] = hi_st<F16>(rv.w);
   } else {
 #pragma unroll
     for (int v = 0; v < 8; ++v) r[v] = 0.0f;
   }
-  // y = bf16(fma(rm, sum, residual)), the rounding the fused small-batch
+  // y = st(fma(rm, sum, residual)), the rounding the fused small-batch
   // decode kernel (dstream.hip) reproduces.
   uint4 o;
-  o.x = pack_bf16x2(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
-  o.y = pack_bf16x2(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
-  o.z = pack_bf16x2(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
-  o.w = pack_bf16x2(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
+  o.x = pack_st2<F16>(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
+  o.y = pack_st2<F16>(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
+  o.z = pack_st2<F16>(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
+  o.w = pack_st2<F16>(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
   *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
 }
 
-void launch_combine_rows(const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
+void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
                          const float* gates, int T, int K, int H, const uint16_t* residual,
                          float rmul, uint16_t* y, hipStream_t s) {
   if (T <= 0) return;
   const int64_t n = (int64_t)T * (H / 8);
-  combine_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(Y, inverse, n_valid, gates, T, K,
-                                                                 H, residual, rmul, y);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  if (f16)
+    combine_rows_kernel<true><<<blocks, 256, 0, s>>>(Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
+  else
+    combine_rows_kernel<false><<<blocks, 256, 0, s>>>(Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 

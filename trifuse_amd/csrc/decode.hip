@@ -256,7 +256,7 @@ void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* rout
     default: decode_logits_generic<<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
   }
   check_hip(hipGetLastError(), "decode logits launch");
-  launch_topk(route_kind, logits, T, E, K, idx, nullptr, gates, s);
+  launch_topk(route_kind, false, logits, T, E, K, idx, nullptr, gates, s);
 }
 
 void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,

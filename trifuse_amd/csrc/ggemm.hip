@@ -9,8 +9,8 @@
 //     (buffer loads with an LDS destination),
 //   * loads BN packed weight rows (4-bit: 32 bytes, 8-bit: 64 bytes of each
 //     row per step) into registers, dequantises them (s*q+b in fp32,
-//     rounded to bf16) and writes them to LDS,
-//   * runs v_mfma_f32_32x32x16_bf16 on the two LDS tiles, each wave owning a
+//     rounded to the storage dtype, bf16 or half) and writes them to LDS,
+//   * runs v_mfma_f32_32x32x16_bf16 (or _f16) on the two LDS tiles, each wave owning a
 //     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane).
 //
 // Pipeline: two LDS stages for each operand. While the MFMAs of step k read
@@ -67,26 +67,40 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gg_rsrc(const void* base, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// 4 bytes (one 32-bit word of an 8-bit weight row) -> 4 bf16 (s*q+b).
+// 4 bytes (one 32-bit word of an 8-bit weight row) -> 4 values s*q+b in the
+// storage dtype (bf16, or half when F16).
+template <bool F16>
 __device__ __forceinline__ uint2 dequant_word_u8(uint32_t w, float s, float b) {
   float d[4];
   dequant4_u8(w, s, b, d);
   uint2 pk;
-  pk.x = pack_bf16x2(d[0], d[1]);
-  pk.y = pack_bf16x2(d[2], d[3]);
+  pk.x = pack_st2<F16>(d[0], d[1]);
+  pk.y = pack_st2<F16>(d[2], d[3]);
   return pk;
 }
 
-// 8 nibbles (one 32-bit word of a 4-bit weight row) -> 8 bf16 (s*q+b).
+// 8 nibbles (one 32-bit word of a 4-bit weight row) -> 8 values s*q+b.
+template <bool F16>
 __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float b) {
   float d[8];
   dequant8(w, s, b, d);
   uint4 pk;
-  pk.x = pack_bf16x2(d[0], d[1]);
-  pk.y = pack_bf16x2(d[2], d[3]);
-  pk.z = pack_bf16x2(d[4], d[5]);
-  pk.w = pack_bf16x2(d[6], d[7]);
+  pk.x = pack_st2<F16>(d[0], d[1]);
+  pk.y = pack_st2<F16>(d[2], d[3]);
+  pk.z = pack_st2<F16>(d[4], d[5]);
+  pk.w = pack_st2<F16>(d[6], d[7]);
   return pk;
+}
+
+// One 32x32x16 MFMA on bf16 or half operands (fp32 accumulators).
+template <bool F16>
+using op8_t = std::conditional_t<F16, f16x8_t, bf16x8_t>;
+template <bool F16>
+__device__ __forceinline__ f32x16_t mfma32(op8_t<F16> a, op8_t<F16> b, f32x16_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // silu(g) * u with the hardware exp and reciprocal (relative error ~1e-7,
@@ -137,7 +151,7 @@ struct RawB {
   uint32_t s[LB], bias[LB];
 };
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS, bool F16>
 __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgArgs args) {
   using C = GgCfg<BM_, BN_, WAVES_M_, WAVES_N_, MODE, BITS>;
   constexpr int CPR_B = C::CPR_B;
@@ -255,12 +269,12 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   auto bstore_word = [&](const RawB<LB>& st, uint16_t* dst, int w) {
     const int i = w / 4, k = w % 4;
     const int q = i * T + tid;
-    const float sc = bf2f((uint16_t)st.s[i]), bi = bf2f((uint16_t)st.bias[i]);
+    const float sc = st2f<F16>((uint16_t)st.s[i]), bi = st2f<F16>((uint16_t)st.bias[i]);
     if constexpr (BITS == 4) {
-      const uint4 pk = dequant_word(word_of(st.b[i], k), sc, bi);
+      const uint4 pk = dequant_word<F16>(word_of(st.b[i], k), sc, bi);
       *reinterpret_cast<uint4*>(&dst[swz(q >> 1, (q & 1) * 4 + k)]) = pk;
     } else {
-      const uint2 pk = dequant_word_u8(word_of(st.b[i], k), sc, bi);
+      const uint2 pk = dequant_word_u8<F16>(word_of(st.b[i], k), sc, bi);
       *reinterpret_cast<uint2*>(&dst[swz(q >> 2, (q & 3) * 2 + (k >> 1)) + (k & 1) * 4]) = pk;
     }
   };
@@ -293,15 +307,15 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   auto compute = [&](auto live_tag, const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt,
                      uint16_t* nB) {
     constexpr bool LIVE = decltype(live_tag)::value;
-    bf16x8_t af[2][MB], bfr[2][NB];
+    op8_t<F16> af[2][MB], bfr[2][NB];
     auto frag = [&](int ks, int slot) {
       const int kc = ks * 2 + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
-        af[slot][i] = *reinterpret_cast<const bf16x8_t*>(&A[swz(wm * C::WM + i * 32 + (lane & 31), kc)]);
+        af[slot][i] = *reinterpret_cast<const op8_t<F16>*>(&A[swz(wm * C::WM + i * 32 + (lane & 31), kc)]);
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        bfr[slot][j] = *reinterpret_cast<const bf16x8_t*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
+        bfr[slot][j] = *reinterpret_cast<const op8_t<F16>*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
     };
     if constexpr (LIVE) frag(0, 0);
 #pragma unroll
@@ -312,7 +326,7 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
         for (int i = 0; i < MB; ++i)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mfma32<F16>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
       }
       if (ks >= 1) {
 #pragma unroll
@@ -371,10 +385,10 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
       if (MODE == kGgGateUp) {
 #pragma unroll
         for (int jb = 0; jb < NB / 2; ++jb)
-          stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2bf(swiglu(acc[i][jb][v], acc[i][jb + NB / 2][v]));
+          stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2st<F16>(swiglu(acc[i][jb][v], acc[i][jb + NB / 2][v]));
       } else {
 #pragma unroll
-        for (int jb = 0; jb < NB; ++jb) stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2bf(acc[i][jb][v]);
+        for (int jb = 0; jb < NB; ++jb) stage[rr * C::SROW + jb * 32 + (lane & 31)] = f2st<F16>(acc[i][jb][v]);
       }
     }
     // Same-wave LDS accesses complete in order: the reads see the writes.
@@ -421,27 +435,32 @@ static unsigned grid_for(int64_t n_routes, int E, int BM, int NT) {
   return (unsigned)total;
 }
 
-template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE, int BITS>
+template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE, int BITS, bool F16>
 static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
   using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS>;
   const int NT = (a.N + C::OUT_COLS - 1) / C::OUT_COLS;
-  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS><<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16>
+      <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
 }
 
-template <int MODE, int BITS>
+template <int MODE, int BITS, bool F16>
 static void launch_tile(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
   if (use_tall(n_routes, E))
-    launch_one<256, 256, 2, 4, MODE, BITS>(a, n_routes, E, s);
+    launch_one<256, 256, 2, 4, MODE, BITS, F16>(a, n_routes, E, s);
   else
-    launch_one<128, 256, 2, 4, MODE, BITS>(a, n_routes, E, s);
+    launch_one<128, 256, 2, 4, MODE, BITS, F16>(a, n_routes, E, s);
 }
 
 template <int MODE>
-static void launch_mode(const GgArgs& a, int bits, int64_t n_routes, int E, hipStream_t s) {
-  if (bits == 8)
-    launch_tile<MODE, 8>(a, n_routes, E, s);
+static void launch_mode(const GgArgs& a, int bits, bool f16, int64_t n_routes, int E, hipStream_t s) {
+  if (bits == 8 && f16)
+    launch_tile<MODE, 8, true>(a, n_routes, E, s);
+  else if (bits == 8)
+    launch_tile<MODE, 8, false>(a, n_routes, E, s);
+  else if (f16)
+    launch_tile<MODE, 4, true>(a, n_routes, E, s);
   else
-    launch_tile<MODE, 4>(a, n_routes, E, s);
+    launch_tile<MODE, 4, false>(a, n_routes, E, s);
 }
 
 static void check_shapes(int N, int Kin, int bits, int64_t x_rows) {
@@ -456,18 +475,18 @@ static void check_shapes(int N, int Kin, int bits, int64_t x_rows) {
 
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         int bits, uint16_t* h, hipStream_t s) {
+                         int bits, bool f16, uint16_t* h, hipStream_t s) {
   if (n_routes <= 0) return;
   check_shapes(N, Kin, bits, rm.nx);
   GgArgs a{};
   a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = gate; a.wb = up;
   a.N = N; a.Kin = Kin; a.out = h;
-  launch_mode<kGgGateUp>(a, bits, n_routes, E, s);
+  launch_mode<kGgGateUp>(a, bits, f16, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM gate/up launch");
 }
 
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, int bits, uint16_t* y_sorted,
+                       const tfm_affine& w, int N, int Kin, int bits, bool f16, uint16_t* y_sorted,
                        hipStream_t s) {
   if (n_routes <= 0) return;
   check_shapes(N, Kin, bits, n_routes);
@@ -475,19 +494,19 @@ void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_rou
   a.x = hsorted; a.x_bytes = (uint32_t)(n_routes * Kin * 2);
   a.rm = RowMap{g.order, nullptr, 1, 0, nullptr}; a.g = g; a.wa = w; a.wb = w; a.N = N;
   a.Kin = Kin; a.out = y_sorted;
-  launch_mode<kGgDown>(a, bits, n_routes, E, s);
+  launch_mode<kGgDown>(a, bits, f16, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM down launch");
 }
 
 void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
-                        int E, const tfm_affine& w, int N, int Kin, int bits, uint16_t* out,
+                        int E, const tfm_affine& w, int N, int Kin, int bits, bool f16, uint16_t* out,
                         hipStream_t s) {
   if (n_routes <= 0) return;
   check_shapes(N, Kin, bits, rm.nx);
   GgArgs a{};
   a.x = x; a.x_bytes = (uint32_t)(rm.nx * Kin * 2); a.rm = rm; a.g = g; a.wa = w; a.wb = w;
   a.N = N; a.Kin = Kin; a.out = out;
-  launch_mode<kGgPlain>(a, bits, n_routes, E, s);
+  launch_mode<kGgPlain>(a, bits, f16, n_routes, E, s);
   check_hip(hipGetLastError(), "grouped GEMM plain launch");
 }
 

@@ -16,7 +16,7 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-template <int C>
+template <int C, bool F16>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       int T, int H, uint16_t* __restrict__ out) {
@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     const uint32_t u[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float a = lo_bf(u[k]), b = hi_bf(u[k]);
+      const float a = lo_st<F16>(u[k]), b = hi_st<F16>(u[k]);
       s = __builtin_fmaf(a, a, s);
       s = __builtin_fmaf(b, b, s);
     }
@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float na = bf2f(f2bf(lo_bf(u[k]) * inv)), nb = bf2f(f2bf(hi_bf(u[k]) * inv));
-      const uint32_t ra = f2bf(lo_bf(g[k]) * na), rb = f2bf(hi_bf(g[k]) * nb);
+      const float na = st2f<F16>(f2st<F16>(lo_st<F16>(u[k]) * inv)), nb = st2f<F16>(f2st<F16>(hi_st<F16>(u[k]) * inv));
+      const uint32_t ra = f2st<F16>(lo_st<F16>(g[k]) * na), rb = f2st<F16>(hi_st<F16>(g[k]) * nb);
       o[k] = ra | (rb << 16);
     }
     os[i] = make_uint4(o[0], o[1], o[2], o[3]);
@@ -62,6 +62,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 }
 
 // Any H % 64 == 0: the same arithmetic with scalar loads.
+template <bool F16>
 __global__ __launch_bounds__(256) void rmsnorm_generic(const uint16_t* __restrict__ x,
                                                        const uint16_t* __restrict__ w, float eps,
                                                        int T, int H, uint16_t* __restrict__ out) {
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(const uint16_t* __restric
   const uint16_t* xr = x + (int64_t)t * H + lane * c;
   float s = 0.0f;
   for (int j = 0; j < c; ++j) {
-    const float v = bf2f(xr[j]);
+    const float v = st2f<F16>(xr[j]);
     s = __builtin_fmaf(v, v, s);
   }
   const float total = readlane_f(wave_tree_sum64(s), 63);
@@ -80,25 +81,34 @@ __global__ __launch_bounds__(256) void rmsnorm_generic(const uint16_t* __restric
   const float inv = 1.0f / sqrtf(mean + eps);
   uint16_t* orow = out + (int64_t)t * H + lane * c;
   for (int j = 0; j < c; ++j) {
-    const float n = bf2f(f2bf(bf2f(xr[j]) * inv));
-    orow[j] = f2bf(bf2f(w[lane * c + j]) * n);
+    const float n = st2f<F16>(f2st<F16>(st2f<F16>(xr[j]) * inv));
+    orow[j] = f2st<F16>(st2f<F16>(w[lane * c + j]) * n);
   }
 }
 
-void launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out,
-                    hipStream_t s) {
-  if (T <= 0) return;
-  if (H % 64 != 0) fail(TFM_E_UNSUPPORTED, "rmsnorm: hidden width must be a multiple of 64");
+template <bool F16>
+static void rmsnorm_dt(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out,
+                       hipStream_t s) {
   const unsigned blocks = (unsigned)((T + 3) / 4);
   switch (H) {
-    case 512: rmsnorm_kernel<8><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    case 1024: rmsnorm_kernel<16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    case 1536: rmsnorm_kernel<24><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    case 2048: rmsnorm_kernel<32><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    case 3072: rmsnorm_kernel<48><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    case 4096: rmsnorm_kernel<64><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
-    default: rmsnorm_generic<<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 512: rmsnorm_kernel<8, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 1024: rmsnorm_kernel<16, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 1536: rmsnorm_kernel<24, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 2048: rmsnorm_kernel<32, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 3072: rmsnorm_kernel<48, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    case 4096: rmsnorm_kernel<64, F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
+    default: rmsnorm_generic<F16><<<blocks, 256, 0, s>>>(x, w, eps, T, H, out); break;
   }
+}
+
+void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, int T, int H,
+                    uint16_t* out, hipStream_t s) {
+  if (T <= 0) return;
+  if (H % 64 != 0) fail(TFM_E_UNSUPPORTED, "rmsnorm: hidden width must be a multiple of 64");
+  if (f16)
+    rmsnorm_dt<true>(x, w, eps, T, H, out, s);
+  else
+    rmsnorm_dt<false>(x, w, eps, T, H, out, s);
   check_hip(hipGetLastError(), "rmsnorm launch");
 }
 

@@ -261,13 +261,69 @@ void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bia
   check_hip(hipGetLastError(), "router_logits launch");
 }
 
+// Affine-quantised router (native_affine_qmm of the router weight,
+// export_native_olmoe_target.py:194-200): the dense router's arithmetic with
+// w[e,h] = st(fmaf(s, q, b)), the dequantised weight rounded to the storage
+// dtype (native_affine_ops.py:29-36). One wave per (token, expert); x and the
+// logits are in the storage dtype (bf16, or half when F16), scales and biases
+// too. Group size 64.
+template <bool F16, int BITS>
+__global__ __launch_bounds__(256) void affine_router_logits_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint32_t* __restrict__ q,
+                                                                   const uint16_t* __restrict__ sc,
+                                                                   const uint16_t* __restrict__ bi,
+                                                                   const float* __restrict__ bias,
+                                                                   int T, int H, int E,
+                                                                   uint16_t* __restrict__ logits) {
+  constexpr int PER = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= (int64_t)T * E) return;  // whole wave exits together
+  const int tok = (int)(wave / E), e = (int)(wave % E);
+  const int c = H / 64;
+  const uint16_t* xr = x + (int64_t)tok * H;
+  const uint32_t* qr = q + (int64_t)e * (H / PER);
+  const uint16_t* sr = sc + (int64_t)e * (H / 64);
+  const uint16_t* br = bi + (int64_t)e * (H / 64);
+  float acc = 0.0f;
+  for (int j = 0; j < c; ++j) {
+    const int k = lane * c + j;
+    const uint32_t code = (qr[k / PER] >> (BITS * (k % PER))) & MASK;
+    const float wv = st2f<F16>(f2st<F16>(__builtin_fmaf(st2f<F16>(sr[k >> 6]), (float)code, st2f<F16>(br[k >> 6]))));
+    acc = __builtin_fmaf(st2f<F16>(xr[k]), wv, acc);
+  }
+  acc = wave_tree_sum64(acc);
+  if (lane == 63) logits[(int64_t)tok * E + e] = f2st<F16>(bias ? acc + bias[e] : acc);
+}
+
+void launch_affine_router_logits(bool f16, int bits, const uint16_t* x, const tfm_affine& w,
+                                 const float* bias, int T, int H, int E, uint16_t* logits,
+                                 hipStream_t s) {
+  if (T <= 0) return;
+  const int64_t waves = (int64_t)T * E;
+  const unsigned blocks = (unsigned)((waves + 3) / 4);
+  const uint32_t* q = static_cast<const uint32_t*>(w.q);
+  const uint16_t* sc = static_cast<const uint16_t*>(w.scales);
+  const uint16_t* bi = static_cast<const uint16_t*>(w.biases);
+  if (f16 && bits == 8)
+    affine_router_logits_kernel<true, 8><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+  else if (f16)
+    affine_router_logits_kernel<true, 4><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+  else if (bits == 8)
+    affine_router_logits_kernel<false, 8><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+  else
+    affine_router_logits_kernel<false, 4><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+  check_hip(hipGetLastError(), "affine router launch");
+}
+
 __device__ __forceinline__ float readlane_f(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
 // One wave per token. gates_native: bf16 probabilities (OLMoE) or fp32
 // (Granite); gates_f32: fp32 copy. Either may be null.
-template <int ROUTE>
+template <int ROUTE, bool F16>
 __global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ logits, int T,
                                                    int E, int K, int32_t* __restrict__ idx,
                                                    void* __restrict__ gates_native,
@@ -280,10 +336,10 @@ __global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ 
   int id;
   if (ROUTE == TFM_ROUTE_OLMOE) {
     uint16_t gb;
-    id = olmoe_route_wave(row, E, K, &g, &gb);
+    id = olmoe_route_wave<F16>(row, E, K, &g, &gb);
     if (lane < K && gates_native) static_cast<uint16_t*>(gates_native)[(int64_t)t * K + lane] = gb;
   } else {
-    id = granite_route_wave(row, E, K, &g);
+    id = granite_route_wave<F16>(row, E, K, &g);
     if (lane < K && gates_native) static_cast<float*>(gates_native)[(int64_t)t * K + lane] = g;
   }
   if (lane < K) {
@@ -295,7 +351,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const uint16_t* __restrict__ 
 // Top-k of kTopkTokensPerBlock tokens per workgroup (one wave per token at a
 // time), plus the histogram of the workgroup's routes over the E experts for
 // the grouping pass (its chunk is kTopkTokensPerBlock * K flat routes).
-template <int ROUTE>
+template <int ROUTE, bool F16>
 __global__ __launch_bounds__(256) void topk_hist_kernel(const uint16_t* __restrict__ logits, int T,
                                                         int E, int K, int32_t* __restrict__ idx,
                                                         float* __restrict__ gates_f32,
@@ -315,9 +371,9 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(const uint16_t* __restri
     int id;
     if (ROUTE == TFM_ROUTE_OLMOE) {
       uint16_t gb;
-      id = olmoe_route_wave(row, E, K, &g, &gb);
+      id = olmoe_route_wave<F16>(row, E, K, &g, &gb);
     } else {
-      id = granite_route_wave(row, E, K, &g);
+      id = granite_route_wave<F16>(row, E, K, &g);
     }
     if (lane < K) {
       idx[(int64_t)t * K + lane] = id;
@@ -329,37 +385,55 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(const uint16_t* __restri
   if (tid <= E) hist[(int64_t)blockIdx.x * (E + 1) + tid] = h[tid];
 }
 
-void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
-                      float* gates_f32, int32_t* hist, hipStream_t s) {
-  if (T <= 0) return;
+template <bool F16>
+static void topk_hist_dt(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                         float* gates_f32, int32_t* hist, hipStream_t s) {
   const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
   if (route_kind == TFM_ROUTE_OLMOE)
-    topk_hist_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+    topk_hist_kernel<TFM_ROUTE_OLMOE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
   else
-    topk_hist_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+    topk_hist_kernel<TFM_ROUTE_GRANITE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+}
+
+void launch_topk_hist(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                      float* gates_f32, int32_t* hist, hipStream_t s) {
+  if (T <= 0) return;
+  if (f16)
+    topk_hist_dt<true>(route_kind, logits, T, E, K, idx, gates_f32, hist, s);
+  else
+    topk_hist_dt<false>(route_kind, logits, T, E, K, idx, gates_f32, hist, s);
   check_hip(hipGetLastError(), "topk_hist launch");
 }
 
-void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
-                 void* gates_native, float* gates_f32, hipStream_t s) {
-  if (T <= 0) return;
+template <bool F16>
+static void topk_dt(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                    void* gates_native, float* gates_f32, hipStream_t s) {
   const unsigned blocks = (unsigned)((T + 3) / 4);
   if (route_kind == TFM_ROUTE_OLMOE)
-    topk_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
+    topk_kernel<TFM_ROUTE_OLMOE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
   else
-    topk_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
+    topk_kernel<TFM_ROUTE_GRANITE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_native, gates_f32);
+}
+
+void launch_topk(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                 void* gates_native, float* gates_f32, hipStream_t s) {
+  if (T <= 0) return;
+  if (f16)
+    topk_dt<true>(route_kind, logits, T, E, K, idx, gates_native, gates_f32, s);
+  else
+    topk_dt<false>(route_kind, logits, T, E, K, idx, gates_native, gates_f32, s);
   check_hip(hipGetLastError(), "topk launch");
 }
 
 // Ranking only (values given): one wave per row.
-template <int RULE>
+template <int RULE, bool F16>
 __global__ __launch_bounds__(256) void rank_topk_kernel(const uint16_t* __restrict__ values, int T,
                                                         int n, int K, int32_t* __restrict__ idx) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // whole wave exits together
   const bool valid = lane < n;
-  const float v = valid ? bf2f(values[(int64_t)t * n + lane]) : 0.0f;
+  const float v = valid ? st2f<F16>(values[(int64_t)t * n + lane]) : 0.0f;
   const bool vn = v != v;
   int rank = 0;
   for (int j = 0; j < n; ++j) {
@@ -377,17 +451,22 @@ __global__ __launch_bounds__(256) void rank_topk_kernel(const uint16_t* __restri
   }
 }
 
-void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
+void launch_rank_topk(int rule, bool f16, const uint16_t* values, int T, int n, int K, int32_t* idx,
                       hipStream_t s) {
   if (T <= 0) return;
   const unsigned blocks = (unsigned)((T + 3) / 4);
-  if (rule == TFM_ROUTE_OLMOE)
-    rank_topk_kernel<TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+  if (rule == TFM_ROUTE_OLMOE && f16)
+    rank_topk_kernel<TFM_ROUTE_OLMOE, true><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+  else if (rule == TFM_ROUTE_OLMOE)
+    rank_topk_kernel<TFM_ROUTE_OLMOE, false><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+  else if (f16)
+    rank_topk_kernel<TFM_ROUTE_GRANITE, true><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
   else
-    rank_topk_kernel<TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
+    rank_topk_kernel<TFM_ROUTE_GRANITE, false><<<blocks, 256, 0, s>>>(values, T, n, K, idx);
   check_hip(hipGetLastError(), "rank_topk launch");
 }
 
+template <bool F16>
 __global__ __launch_bounds__(256) void olmoe_softmax_kernel(const uint16_t* __restrict__ logits,
                                                             int T, int E,
                                                             uint16_t* __restrict__ probs) {
@@ -395,15 +474,18 @@ __global__ __launch_bounds__(256) void olmoe_softmax_kernel(const uint16_t* __re
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // whole wave exits together
   const bool valid = lane < E;
-  const float ld = valid ? bf2f(logits[(int64_t)t * E + lane]) : -__builtin_inff();
+  const float ld = valid ? st2f<F16>(logits[(int64_t)t * E + lane]) : -__builtin_inff();
   float norm;
   const float ex = wave_softmax_exp(ld, &norm);
-  if (valid) probs[(int64_t)t * E + lane] = f2bf(ex * norm);
+  if (valid) probs[(int64_t)t * E + lane] = f2st<F16>(ex * norm);
 }
 
-void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s) {
+void launch_olmoe_softmax(bool f16, const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s) {
   if (T <= 0) return;
-  olmoe_softmax_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(logits, T, E, probs);
+  if (f16)
+    olmoe_softmax_kernel<true><<<(unsigned)((T + 3) / 4), 256, 0, s>>>(logits, T, E, probs);
+  else
+    olmoe_softmax_kernel<false><<<(unsigned)((T + 3) / 4), 256, 0, s>>>(logits, T, E, probs);
   check_hip(hipGetLastError(), "olmoe_softmax launch");
 }
 

@@ -87,18 +87,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// OLMoE routing of one token. row: E bf16 logits. Lane s < K of the wave
-// returns slot s's expert id and gate (others return -1 / 0); the bf16 gate
-// bits come back in *gate_bits.
+// OLMoE routing of one token. row: E logits in the storage dtype (bf16, or
+// half when F16). Lane s < K of the wave returns slot s's expert id and gate
+// (others return -1 / 0); the gate's storage bits come back in *gate_bits.
+template <bool F16 = false>
 __device__ __forceinline__ int olmoe_route_wave(const uint16_t* __restrict__ row, int E, int K,
                                                 float* gate, uint16_t* gate_bits) {
   const int lane = threadIdx.x & 63;
   const bool valid = lane < E;
-  const float ld = valid ? bf2f(row[lane]) : -__builtin_inff();
+  const float ld = valid ? st2f<F16>(row[lane]) : -__builtin_inff();
   float norm;
   const float ex = wave_softmax_exp(ld, &norm);
-  const uint16_t pb = f2bf(ex * norm);
-  const float p = bf2f(pb);
+  const uint16_t pb = f2st<F16>(ex * norm);
+  const float p = st2f<F16>(pb);
   // NaN ranks after every number: key 0, below sortable(-inf) = 0x007fffff.
   uint32_t key = p != p ? 0u : sortable_key(p);
   bool removed = !valid;
@@ -126,11 +127,12 @@ __device__ __forceinline__ int olmoe_route_wave(const uint16_t* __restrict__ row
 
 // Granite routing of one token. Lane s < K returns slot s's expert id and fp32
 // gate; other lanes return -1.
+template <bool F16 = false>
 __device__ __forceinline__ int granite_route_wave(const uint16_t* __restrict__ row, int E, int K,
                                                   float* gate) {
   const int lane = threadIdx.x & 63;
   const bool valid = lane < E;
-  const float v = valid ? bf2f(row[lane]) : 0.0f;
+  const float v = valid ? st2f<F16>(row[lane]) : 0.0f;
   // NaN ranks above every number: key ~0u.
   const uint32_t key = v != v ? 0xffffffffu : sortable_key(v);
   bool removed = !valid;

@@ -9,6 +9,7 @@ namespace tfm {
 constexpr int kWave = 64;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -30,6 +31,57 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   v[0] = (__bf16)a;
   v[1] = (__bf16)b;
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// IEEE half bits to float (exact).
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Float to IEEE half bits, round to nearest even (subnormal results included,
+// overflow to infinity, NaN kept quiet with its sign). Integer arithmetic, so
+// the result does not depend on the hardware denormal mode.
+__device__ __forceinline__ uint16_t f2h(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // |f| >= 65520 rounds to infinity
+  if (a >= 0x38800000u) {                                    // normal half: rebias 127 -> 15
+    const uint32_t r = a - 0x38000000u;
+    return (uint16_t)(sign | ((r + 0xfffu + ((r >> 13) & 1u)) >> 13));
+  }
+  if (a <= 0x33000000u) return (uint16_t)sign;               // |f| <= 2^-25 rounds to zero
+  const uint32_t m = (a & 0x7fffffu) | 0x800000u;            // subnormal half: units of 2^-24
+  const int sh = 126 - (int)(a >> 23);                       // 14 .. 24
+  uint32_t q = m >> sh;
+  const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+  return (uint16_t)(sign | q);
+}
+
+// Activation storage of the block: bf16 (F16 = false) or IEEE half, as bits.
+template <bool F16>
+__device__ __forceinline__ float st2f(uint16_t h) { return F16 ? h2f(h) : bf2f(h); }
+template <bool F16>
+__device__ __forceinline__ uint16_t f2st(float f) { return F16 ? f2h(f) : f2bf(f); }
+
+// Two floats to packed half (low = a), hardware round-to-nearest-even.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  f16x2_t v;
+  v[0] = (_Float16)a;
+  v[1] = (_Float16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Low/high 16-bit half of a word in the storage dtype, to float.
+template <bool F16>
+__device__ __forceinline__ float lo_st(uint32_t w) { return F16 ? h2f((uint16_t)(w & 0xffffu)) : __uint_as_float(w << 16); }
+template <bool F16>
+__device__ __forceinline__ float hi_st(uint32_t w) { return F16 ? h2f((uint16_t)(w >> 16)) : __uint_as_float(w & 0xffff0000u); }
+
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_st2(float a, float b) {
+  return F16 ? pack_f16x2(a, b) : pack_bf16x2(a, b);
 }
 
 // Word k (0..3) of a 16-byte vector.

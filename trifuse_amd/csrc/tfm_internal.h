@@ -61,11 +61,17 @@ struct Grouping {
 // ---- launchers (defined in the .hip files) ----
 void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int T,
                           int H, int E, uint16_t* logits, hipStream_t s);
-void launch_topk(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+// f16: logits/values/probabilities are IEEE half bits instead of bf16.
+void launch_topk(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,
                  void* gates_native, float* gates_f32, hipStream_t s);
-void launch_rank_topk(int rule, const uint16_t* values, int T, int n, int K, int32_t* idx,
+void launch_rank_topk(int rule, bool f16, const uint16_t* values, int T, int n, int K, int32_t* idx,
                       hipStream_t s);
-void launch_olmoe_softmax(const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
+void launch_olmoe_softmax(bool f16, const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
+// Affine-quantised router [E, H] (bits 4 or 8, group 64): logits in the
+// storage dtype with the dense router's bit-defined order.
+void launch_affine_router_logits(bool f16, int bits, const uint16_t* x, const tfm_affine& w,
+                                 const float* bias, int T, int H, int E, uint16_t* logits,
+                                 hipStream_t s);
 // Grouping (group.hip): per-chunk expert histograms, then a stable scatter.
 // hist holds group_blocks(n, chunk) rows of E+1 counts (bucket E: bad ids).
 constexpr int kGroupChunk = 512;           // routes per chunk for given routes
@@ -86,13 +92,13 @@ void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, int32
 bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
                         int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
                         uint16_t* logits_out, hipStream_t s);
-void launch_topk_hist(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+void launch_topk_hist(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,
                       float* gates_f32, int32_t* hist, hipStream_t s);
 
-// Post-attention RMSNorm (norm.hip): out = bf16(w * bf16(x * inv)), one wave
-// per row, bit-defined order.
-void launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out,
-                    hipStream_t s);
+// Post-attention RMSNorm (norm.hip): out = st(w * st(x * inv)) in the storage
+// dtype (bf16, or half when f16), one wave per row, bit-defined order.
+void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, int T, int H,
+                    uint16_t* out, hipStream_t s);
 
 // Decode path (decode.hip), T*K <= 256 routes.
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
@@ -169,12 +175,12 @@ void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_acti
 //   plain:  out[order[j], :] = bf16(x W^T)                 (gather_qmm)
 void launch_ggemm_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
                          int E, const tfm_affine& gate, const tfm_affine& up, int N, int Kin,
-                         int bits, uint16_t* h, hipStream_t s);
+                         int bits, bool f16, uint16_t* h, hipStream_t s);
 void launch_ggemm_down(const uint16_t* hsorted, const Grouping& g, int64_t n_routes, int E,
-                       const tfm_affine& w, int N, int Kin, int bits, uint16_t* y_sorted,
+                       const tfm_affine& w, int N, int Kin, int bits, bool f16, uint16_t* y_sorted,
                        hipStream_t s);
 void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t n_routes,
-                        int E, const tfm_affine& w, int N, int Kin, int bits, uint16_t* out,
+                        int E, const tfm_affine& w, int N, int Kin, int bits, bool f16, uint16_t* out,
                         hipStream_t s);
 
 // Combine of gate-weighted fp32 rows (decode path):
@@ -186,7 +192,7 @@ void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t
 // Combine of bf16 expert-output rows (prefill path):
 //   y[t, c] = bf16(residual[t, c] + rm * sum_k gate[t*K+k] * Y[inverse[t*K+k], c])
 // with the same k order and bad-route rule.
-void launch_combine_rows(const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
+void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, const int32_t* n_valid,
                          const float* gates, int T, int K, int H, const uint16_t* residual,
                          float rmul, uint16_t* y, hipStream_t s);
 // Expert-sorted output rows for the hook (decode path): out[j, c] = bf16(P[j, c])

@@ -29,8 +29,9 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import (TFM_DTYPE_BF16, TFM_FLAG_DETERMINISTIC, TFM_ROUTE_GRANITE, TFM_ROUTE_OLMOE,
-                   TFM_ROUTER_DENSE, Affine, Geometry, MoeWeights, call)
+from ._lib import (TFM_DTYPE_BF16, TFM_DTYPE_F16, TFM_FLAG_DETERMINISTIC, TFM_ROUTE_GRANITE,
+                   TFM_ROUTE_OLMOE, TFM_ROUTER_AFFINE, TFM_ROUTER_DENSE, Affine, Geometry,
+                   MoeWeights, call)
 
 _ROUTES = {"olmoe": TFM_ROUTE_OLMOE, "granite": TFM_ROUTE_GRANITE}
 _PACKED = (torch.int32, torch.uint32)
@@ -90,9 +91,20 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def _check_bf16(t: torch.Tensor, name: str) -> None:
-    if t.dtype != torch.bfloat16:
-        raise NotImplementedError(f"{name}: only bf16 activations/scales are built (got {t.dtype})")
+_DTYPES = {torch.bfloat16: TFM_DTYPE_BF16, torch.float16: TFM_DTYPE_F16}
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    """C-ABI storage dtype of t: bf16 or IEEE half."""
+    code = _DTYPES.get(t.dtype)
+    if code is None:
+        raise NotImplementedError(f"{name}: only bf16 and f16 storage are built (got {t.dtype})")
+    return code
+
+
+def _check_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype} differs from the block's {dtype}")
 
 
 # ---------------------------------------------------------------------------
@@ -104,10 +116,11 @@ def gather_qmm_rows(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, bias
                     sorted_indices: bool = False, group_size: int = 64, bits: int = 4) -> torch.Tensor:
     """out[r] = x[x_rows[r]] . dequant(W[rhs_indices[r]])^T for r in [0, len(rhs_indices)).
 
-    x [X, Kin] bf16; q [E, N, Kin/8]; x_rows None means identity."""
+    x [X, Kin] bf16 or f16 (scales and biases in the same dtype);
+    q [E, N, Kin*bits/32]; x_rows None means identity."""
     kin = validate_affine(q, scales, biases, group_size, bits, 3)
-    _check_bf16(x, "x")
-    _check_bf16(scales, "scales")
+    dt = _dtype_code(x, "x")
+    _check_dtype(scales, x.dtype, "scales")
     _dev(x, "x")
     if x.ndim != 2 or x.shape[1] != kin:
         raise ValueError("Native affine expert input differs")
@@ -123,7 +136,7 @@ def gather_qmm_rows(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, bias
     ws = _workspace(wsb, x.device)
     aff = _affine(q, scales, biases)
     call("tfm_gather_qmm", x.data_ptr(), x.shape[0], _ptr(xr), _ptr(rhs), rows, ctypes.byref(aff),
-         E, N, kin, group_size, bits, TFM_DTYPE_BF16, int(bool(sorted_indices)), out.data_ptr(),
+         E, N, kin, group_size, bits, dt, int(bool(sorted_indices)), out.data_ptr(),
          ws.data_ptr(), ws.numel(), _stream())
     return out
 
@@ -188,26 +201,27 @@ def native_affine_qmm(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, bi
 
 def native_olmoe_softmax(x: torch.Tensor) -> torch.Tensor:
     """mlx::native_olmoe_softmax (native_affine_ops.py:128-138): precise fp32
-    softmax over the last axis, rounded to the storage dtype. x is [1, T, E]."""
-    if x.ndim != 3 or x.dtype != torch.bfloat16:
-        raise ValueError("OLMoE router requires B1/T/E BF16 logits")
+    softmax over the last axis, rounded to the storage dtype. x is [1, T, E],
+    FP16 as the reference requires, or BF16."""
+    if x.ndim != 3 or x.dtype not in _DTYPES:
+        raise ValueError("OLMoE router requires B1/T/E FP16 (or BF16) logits")
     _dev(x, "x")
     E = x.shape[-1]
     rows = x.numel() // E
     out = torch.empty_like(x)
-    call("tfm_olmoe_softmax", x.data_ptr(), rows, E, TFM_DTYPE_BF16, out.data_ptr(), _stream())
+    call("tfm_olmoe_softmax", x.data_ptr(), rows, E, _DTYPES[x.dtype], out.data_ptr(), _stream())
     return out
 
 
 def _topk(x: torch.Tensor, k: int, rule: int) -> torch.Tensor:
     if type(k) is not int or not 0 < k <= x.shape[-1]:
         raise ValueError("Invalid top-k")
-    _check_bf16(x, "x")
+    dt = _dtype_code(x, "x")
     _dev(x, "x")
     n = x.shape[-1]
     rows = x.numel() // n
     out = torch.empty((*x.shape[:-1], k), dtype=torch.int32, device=x.device)
-    call("tfm_topk", x.data_ptr(), rows, n, k, rule, TFM_DTYPE_BF16, out.data_ptr(), _stream())
+    call("tfm_topk", x.data_ptr(), rows, n, k, rule, dt, out.data_ptr(), _stream())
     return out
 
 
@@ -215,7 +229,7 @@ def native_olmoe_topk_indices(x: torch.Tensor, k: int) -> torch.Tensor:
     """mlx::native_olmoe_topk_indices (native_affine_ops.py:141-153) as lowered
     (native_affine_lowering.py:93-108): the k largest values in descending
     order, ties to the lower index, NaN last."""
-    if x.ndim != 3 or x.dtype != torch.bfloat16 or type(k) is not int or not 0 < k <= x.shape[-1]:
+    if x.ndim != 3 or x.dtype not in _DTYPES or type(k) is not int or not 0 < k <= x.shape[-1]:
         raise ValueError("Invalid OLMoE probability/top-k ABI")
     return _topk(x, k, TFM_ROUTE_OLMOE)
 
@@ -244,9 +258,10 @@ def native_take_along_last(x: torch.Tensor, indices: torch.Tensor) -> torch.Tens
 @dataclasses.dataclass
 class ExpertWeights:
     """Stacked switch_mlp weights of one layer (prepare_model.py:67-106 layout):
-    gate/up Q [E, I, H/8], S/B [E, I, H/64]; down Q [E, H, I/8], S/B [E, H, I/64];
-    router [E, H] (dense); logit_bias optional fp32 [E]."""
-    router: torch.Tensor
+    gate/up Q [E, I, H*bits/32], S/B [E, I, H/64]; down Q [E, H, I*bits/32],
+    S/B [E, H, I/64]; router [E, H] (dense router) or router_q [E, H*router_bits/32],
+    router_s/router_b [E, H/64] (affine router); logit_bias optional fp32 [E]."""
+    router: Optional[torch.Tensor]
     gate_q: torch.Tensor
     gate_s: torch.Tensor
     gate_b: torch.Tensor
@@ -257,10 +272,15 @@ class ExpertWeights:
     down_s: torch.Tensor
     down_b: torch.Tensor
     logit_bias: Optional[torch.Tensor] = None
+    router_q: Optional[torch.Tensor] = None
+    router_s: Optional[torch.Tensor] = None
+    router_b: Optional[torch.Tensor] = None
+    router_bits: int = 4
 
     @classmethod
     def from_layer(cls, layer) -> "ExpertWeights":
-        return cls(**{f.name: getattr(layer, f.name) for f in dataclasses.fields(cls)})
+        return cls(**{f.name: getattr(layer, f.name) for f in dataclasses.fields(cls)
+                      if hasattr(layer, f.name)})
 
 
 class MoEBlock:
@@ -269,9 +289,16 @@ class MoEBlock:
 
     def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int,
                  experts_per_token: int, route: str = "olmoe", residual_multiplier: float = 1.0,
-                 group_size: int = 64, bits: int = 4):
+                 group_size: int = 64, bits: int = 4, dtype: torch.dtype = torch.bfloat16,
+                 router: str = "dense"):
         if route not in _ROUTES:
             raise ValueError(f"unknown route kind {route!r}")
+        if dtype not in _DTYPES:
+            raise ValueError(f"unknown storage dtype {dtype}")
+        if router not in ("dense", "affine"):
+            raise ValueError(f"unknown router kind {router!r}")
+        self.dtype = dtype
+        self.router_kind = router
         self.hidden_size = hidden_size
         self.intermediate_size = intermediate_size
         self.num_experts = num_experts
@@ -280,7 +307,8 @@ class MoEBlock:
         self.residual_multiplier = residual_multiplier
         self.bits = bits
         self.geometry = Geometry(hidden_size, intermediate_size, num_experts, experts_per_token,
-                                 group_size, bits, TFM_DTYPE_BF16, _ROUTES[route], TFM_ROUTER_DENSE,
+                                 group_size, bits, _DTYPES[dtype], _ROUTES[route],
+                                 TFM_ROUTER_DENSE if router == "dense" else TFM_ROUTER_AFFINE,
                                  float(residual_multiplier))
         lib = _lib.load()
         handle = ctypes.c_void_p()
@@ -327,13 +355,13 @@ class MoEBlock:
     # -- checks --------------------------------------------------------------
     def _check_x(self, x: torch.Tensor) -> int:
         _dev(x, "x")
-        _check_bf16(x, "x")
+        _check_dtype(x, self.dtype, "x")
         if x.shape[-1] != self.hidden_size:
             raise ValueError("hidden width differs")
         return x.numel() // self.hidden_size
 
     _WEIGHT_FIELDS = ("router", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q",
-                      "down_s", "down_b", "logit_bias")
+                      "down_s", "down_b", "logit_bias", "router_q", "router_s", "router_b")
 
     def _weights(self, w: ExpertWeights, router: bool) -> MoeWeights:
         """Validated C-ABI weight struct of `w`, cached per weights object while
@@ -365,14 +393,24 @@ class MoEBlock:
         validate_affine(w.up_q, w.up_s, w.up_b, 64, self.bits, 3)
         validate_affine(w.down_q, w.down_s, w.down_b, 64, self.bits, 3)
         for name in ("gate_s", "up_s", "down_s"):
-            _check_bf16(getattr(w, name), name)
+            _check_dtype(getattr(w, name), self.dtype, name)
         mw = MoeWeights()
         mw.gate = _affine(w.gate_q, w.gate_s, w.gate_b)
         mw.up = _affine(w.up_q, w.up_s, w.up_b)
         mw.down = _affine(w.down_q, w.down_s, w.down_b)
-        if router:
+        if router and self.router_kind == "affine":
+            rb = w.router_bits
+            if w.router_q is None or w.router_s is None or w.router_b is None:
+                raise ValueError("affine router needs router_q, router_s and router_b")
+            width = validate_affine(w.router_q, w.router_s, w.router_b, 64, rb, 2)
+            if width != H or w.router_q.shape[0] != E:
+                raise ValueError("router shape differs")
+            _check_dtype(w.router_s, self.dtype, "router_s")
+            mw.router_affine = _affine(w.router_q, w.router_s, w.router_b)
+            mw.router_bits = rb
+        elif router:
             _dev(w.router, "router")
-            _check_bf16(w.router, "router")
+            _check_dtype(w.router, self.dtype, "router")
             if tuple(w.router.shape) != (E, H):
                 raise ValueError("router shape differs")
             mw.router = w.router.data_ptr()
@@ -414,7 +452,7 @@ class MoEBlock:
         With return_routes, also returns (idx [T,K] int32, gates [T,K] fp32)."""
         T = self._check_x(h)
         _dev(norm_weight, "norm_weight")
-        _check_bf16(norm_weight, "norm_weight")
+        _check_dtype(norm_weight, self.dtype, "norm_weight")
         if norm_weight.numel() != self.hidden_size or not norm_weight.is_contiguous():
             raise ValueError("norm_weight must be a contiguous [H] tensor")
         mw = self._weights(weights, router=True)
@@ -435,16 +473,39 @@ class MoEBlock:
         OLMoE gates are bf16 probabilities; Granite gates are fp32."""
         T = self._check_x(x)
         _dev(router, "router")
-        _check_bf16(router, "router")
+        _check_dtype(router, self.dtype, "router")
         K, E = self.experts_per_token, self.num_experts
         idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
-        gdt = torch.bfloat16 if self.route_kind == "olmoe" else torch.float32
+        gdt = self.dtype if self.route_kind == "olmoe" else torch.float32
         gates = torch.empty((T, K), dtype=gdt, device=x.device)
-        logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
+        logits = torch.empty((T, E), dtype=self.dtype, device=x.device)
         if logit_bias is not None:
             _dev(logit_bias, "logit_bias")
         ws = self.workspace(T, x.device)
         call("tfm_route", self._plan, x.data_ptr(), T, router.data_ptr(), _ptr(logit_bias),
+             logits.data_ptr(), idx.data_ptr(), gates.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+        return idx, gates, logits
+
+    def route_affine(self, x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     bits: int = 4, logit_bias: Optional[torch.Tensor] = None):
+        """Affine-quantised router linear + routing (the exports' router
+        Affine module, export_native_olmoe_target.py:194-202): (idx [T,K] int32,
+        gates [T,K], logits [T,E] in the block's dtype)."""
+        T = self._check_x(x)
+        K, E = self.experts_per_token, self.num_experts
+        width = validate_affine(q, scales, biases, 64, bits, 2)
+        if width != self.hidden_size or q.shape[0] != E:
+            raise ValueError("router shape differs")
+        _check_dtype(scales, self.dtype, "scales")
+        idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+        gdt = self.dtype if self.route_kind == "olmoe" else torch.float32
+        gates = torch.empty((T, K), dtype=gdt, device=x.device)
+        logits = torch.empty((T, E), dtype=self.dtype, device=x.device)
+        if logit_bias is not None:
+            _dev(logit_bias, "logit_bias")
+        aff = _affine(q, scales, biases)
+        ws = self.workspace(T, x.device)
+        call("tfm_route_affine", self._plan, x.data_ptr(), T, ctypes.byref(aff), bits, _ptr(logit_bias),
              logits.data_ptr(), idx.data_ptr(), gates.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
         return idx, gates, logits
 

@@ -121,17 +121,17 @@ def packed_nibbles(shape, key: int, device) -> torch.Tensor:
     return _as_int32(hash_u32(n, key, device)).reshape(shape)
 
 
-def uniform_scales(shape, key: int, device, lo=0.005, hi=0.02) -> torch.Tensor:
+def uniform_scales(shape, key: int, device, lo=0.005, hi=0.02, dtype=torch.bfloat16) -> torch.Tensor:
     n = int(np.prod(shape))
     u = (hash_u32(n, key, device) >> 8).to(torch.float32) * (1.0 / (1 << 24))
     s = torch.tensor(lo, dtype=torch.float32) + torch.tensor(hi - lo, dtype=torch.float32).to(device) * u
-    return s.to(torch.bfloat16).reshape(shape)
+    return s.to(dtype).reshape(shape)
 
 
-def normal_bf16(shape, sigma: float, key: int) -> torch.Tensor:
+def normal_bf16(shape, sigma: float, key: int, dtype=torch.bfloat16) -> torch.Tensor:
     rng = np.random.Generator(np.random.PCG64(np.random.SeedSequence([SEED, key])))
     v = rng.standard_normal(size=int(np.prod(shape)), dtype=np.float64) * sigma
-    return torch.from_numpy(v.astype(np.float32)).to(torch.bfloat16).reshape(shape)
+    return torch.from_numpy(v.astype(np.float32)).to(dtype).reshape(shape)
 
 
 def zipf_bias(experts: int, key: int, s: float = 1.1, alpha: float = 0.875) -> torch.Tensor:
@@ -142,7 +142,7 @@ def zipf_bias(experts: int, key: int, s: float = 1.1, alpha: float = 0.875) -> t
 
 @dataclasses.dataclass
 class LayerWeights:
-    router: torch.Tensor          # [E, H] bf16
+    router: Optional[torch.Tensor]  # [E, H] dense router (None with an affine router)
     gate_q: torch.Tensor          # [E, I, H/8] int32 (uint32 bits)
     gate_s: torch.Tensor          # [E, I, H/64] bf16
     gate_b: torch.Tensor
@@ -153,40 +153,62 @@ class LayerWeights:
     down_s: torch.Tensor          # [E, H, I/64]
     down_b: torch.Tensor
     logit_bias: Optional[torch.Tensor] = None  # [E] fp32
+    router_q: Optional[torch.Tensor] = None    # affine router [E, H*router_bits/32]
+    router_s: Optional[torch.Tensor] = None    # [E, H/64]
+    router_b: Optional[torch.Tensor] = None
+    router_bits: int = 4
 
     def to(self, device) -> "LayerWeights":
-        kw = {f.name: (getattr(self, f.name).to(device) if getattr(self, f.name) is not None else None)
-              for f in dataclasses.fields(self)}
+        kw = {f.name: (v.to(device) if isinstance(v, torch.Tensor) else v)
+              for f in dataclasses.fields(self) for v in (getattr(self, f.name),)}
         return LayerWeights(**kw)
 
     def tensors(self) -> List[torch.Tensor]:
-        return [getattr(self, f.name) for f in dataclasses.fields(self) if getattr(self, f.name) is not None]
+        return [v for f in dataclasses.fields(self) for v in (getattr(self, f.name),)
+                if isinstance(v, torch.Tensor)]
 
 
 def make_layer(geom: Geometry, layer: int, device="cpu", zipf: bool = False,
-               seed_tag: str = "", bits: int = 4) -> LayerWeights:
+               seed_tag: str = "", bits: int = 4, dtype=torch.bfloat16,
+               affine_router: bool = False) -> LayerWeights:
     """Synthetic layer. Codes are uniform over [0, 2^bits) and the bias is
     -2^(bits-1) * scale, so weights are centred on zero; 8-bit scales are
-    1/16 of the 4-bit ones, which keeps the weight range the same."""
+    1/16 of the 4-bit ones, which keeps the weight range the same. Scales,
+    biases and the dense router are in `dtype` (bf16 or f16). With
+    affine_router the router is a 4-bit affine matrix (scales U[0.002, 0.006])
+    instead of a dense one."""
     if bits not in (4, 8):
         raise ValueError("bits must be 4 or 8")
     E, H, I = geom.experts, geom.hidden, geom.intermediate
-    tag = (geom.name, seed_tag, layer) if bits == 4 else (geom.name, seed_tag, layer, bits)
+    tag = (geom.name, seed_tag, layer)
+    if bits != 4:
+        tag = tag + (bits,)
+    if dtype != torch.bfloat16:
+        tag = tag + (str(dtype),)
     w = {}
-    w["router"] = normal_bf16((E, H), 0.02, _key(*tag, "router")).to(device)
     shrink = 16.0 / (1 << bits)
     for proj, (N, Kin) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
         w[f"{proj}_q"] = packed_nibbles((E, N, Kin * bits // 32), _key(*tag, proj, "q"), device)
         s = uniform_scales((E, N, Kin // GROUP), _key(*tag, proj, "s"), device,
-                           lo=0.005 * shrink, hi=0.02 * shrink)
+                           lo=0.005 * shrink, hi=0.02 * shrink, dtype=dtype)
         w[f"{proj}_s"] = s
-        w[f"{proj}_b"] = (s.float() * -float(1 << (bits - 1))).to(torch.bfloat16)
+        w[f"{proj}_b"] = (s.float() * -float(1 << (bits - 1))).to(dtype)
+    if affine_router:
+        w["router"] = None
+        w["router_q"] = packed_nibbles((E, H // 8), _key(*tag, "router", "q"), device)
+        rs = uniform_scales((E, H // GROUP), _key(*tag, "router", "s"), device, lo=0.002, hi=0.006,
+                            dtype=dtype)
+        w["router_s"] = rs
+        w["router_b"] = (rs.float() * -8.0).to(dtype)
+        w["router_bits"] = 4
+    else:
+        w["router"] = normal_bf16((E, H), 0.02, _key(*tag, "router"), dtype).to(device)
     lb = zipf_bias(E, _key(*tag, "zipf")).to(device) if zipf else None
     return LayerWeights(logit_bias=lb, **w)
 
 
-def make_x(geom: Geometry, tokens: int, tag: str = "x") -> torch.Tensor:
-    return normal_bf16((tokens, geom.hidden), 1.0, _key(geom.name, tag, tokens))
+def make_x(geom: Geometry, tokens: int, tag: str = "x", dtype=torch.bfloat16) -> torch.Tensor:
+    return normal_bf16((tokens, geom.hidden), 1.0, _key(geom.name, tag, tokens), dtype)
 
 
 def workload_layers(wl: Workload, device="cpu", layers: Optional[int] = None) -> List[LayerWeights]:
