@@ -121,6 +121,7 @@ struct BlockWs {
   int4* slots;    // decode: per active slot {expert, first route, end route, 0}
   float* gates_sorted;  // decode: gates in sorted order
   uint16_t* xn;         // RMSNorm-ed input [T, H] (tfm_moe_forward_rmsnorm)
+  uint16_t* router_w;   // affine router dequantised to [E, H] (TFM_ROUTER_AFFINE)
   size_t bytes;
 };
 
@@ -145,6 +146,8 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
   w.slots = c.take<int4>((size_t)g.num_experts);
   w.gates_sorted = c.take<float>((size_t)R);
   w.xn = c.take<uint16_t>((size_t)(T * g.hidden_size));
+  if (g.router == TFM_ROUTER_AFFINE)
+    w.router_w = c.take<uint16_t>((size_t)g.num_experts * (size_t)g.hidden_size);
   w.bytes = align_up(c.offset, 256);
   return w;
 }
@@ -364,7 +367,7 @@ int tfm_route(const tfm_plan* plan, const void* x, int64_t tokens, const void* r
     need_ws(workspace, workspace_bytes, ws.bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : ws.logits;
-    launch_router_logits(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router),
+    launch_router_logits(false, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router),
                          logit_bias, (int)tokens, g.hidden_size, g.num_experts, lg, s);
     launch_topk(g.route, false, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates,
                 nullptr, s);
@@ -391,8 +394,9 @@ int tfm_route_affine(const tfm_plan* plan, const void* x, int64_t tokens, const 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f16 = g.dtype == TFM_DTYPE_F16;
     uint16_t* lg = logits ? static_cast<uint16_t*>(logits) : ws.logits;
-    launch_affine_router_logits(f16, router_bits, static_cast<const uint16_t*>(x), *router, logit_bias,
-                                (int)tokens, g.hidden_size, g.num_experts, lg, s);
+    launch_dequant_router(f16, router_bits, *router, g.num_experts, g.hidden_size, ws.router_w, s);
+    launch_router_logits(f16, static_cast<const uint16_t*>(x), ws.router_w, logit_bias, (int)tokens,
+                         g.hidden_size, g.num_experts, lg, s);
     launch_topk(g.route, f16, lg, (int)tokens, g.num_experts, g.experts_per_token, idx, gates, nullptr, s);
   });
 }
@@ -621,22 +625,20 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const bool f16 = g.dtype == TFM_DTYPE_F16;
   bool fused_route = false;
   {
-    // Dense router: router linear, top-k and chunk histograms in one kernel
-    // where the hidden size has a variant; otherwise logits then top-k.
+    // Router linear, top-k and chunk histograms in one kernel where the
+    // hidden size has a variant; otherwise logits then top-k. An affine
+    // router is first dequantised to a dense matrix in the workspace.
     StageScope st(TFM_STAGE_ROUTER, s);
+    const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
     if (g.router == TFM_ROUTER_AFFINE) {
-      launch_affine_router_logits(f16, weights->router_bits, static_cast<const uint16_t*>(x),
-                                  weights->router_affine, weights->logit_bias, T, H, E, ws.logits, s);
-    } else {
-      fused_route = launch_router_topk(g.route, static_cast<const uint16_t*>(x),
-                                       static_cast<const uint16_t*>(weights->router),
-                                       weights->logit_bias, T, g.hidden_size, E, K, ws.idx, ws.gates,
-                                       ws.hist, nullptr, s);
-      if (!fused_route)
-        launch_router_logits(static_cast<const uint16_t*>(x),
-                             static_cast<const uint16_t*>(weights->router), weights->logit_bias,
-                             (int)tokens, g.hidden_size, g.num_experts, ws.logits, s);
+      launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
+      rw = ws.router_w;
     }
+    fused_route = launch_router_topk(g.route, f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias,
+                                     T, H, E, K, ws.idx, ws.gates, ws.hist, nullptr, s);
+    if (!fused_route)
+      launch_router_logits(f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, (int)tokens, H, E,
+                           ws.logits, s);
   }
   if (!fused_route) {
     StageScope st(TFM_STAGE_TOPK, s);

@@ -18,7 +18,7 @@
 namespace tfm {
 
 // One wave per (token tile of TW tokens, expert tile of EPW experts).
-template <int C, int TW>
+template <int C, int TW, bool F16>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
                                                             const float* __restrict__ bias,
@@ -39,10 +39,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
 #pragma unroll
       for (int i = 0; i < C / 8; ++i) {
         const uint4 v = src[i];
-        xv[t][8 * i + 0] = lo_bf(v.x); xv[t][8 * i + 1] = hi_bf(v.x);
-        xv[t][8 * i + 2] = lo_bf(v.y); xv[t][8 * i + 3] = hi_bf(v.y);
-        xv[t][8 * i + 4] = lo_bf(v.z); xv[t][8 * i + 5] = hi_bf(v.z);
-        xv[t][8 * i + 6] = lo_bf(v.w); xv[t][8 * i + 7] = hi_bf(v.w);
+        xv[t][8 * i + 0] = lo_st<F16>(v.x); xv[t][8 * i + 1] = hi_st<F16>(v.x);
+        xv[t][8 * i + 2] = lo_st<F16>(v.y); xv[t][8 * i + 3] = hi_st<F16>(v.y);
+        xv[t][8 * i + 4] = lo_st<F16>(v.z); xv[t][8 * i + 5] = hi_st<F16>(v.z);
+        xv[t][8 * i + 6] = lo_st<F16>(v.w); xv[t][8 * i + 7] = hi_st<F16>(v.w);
       }
     } else {
 #pragma unroll
@@ -56,10 +56,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
 #pragma unroll
     for (int i = 0; i < C / 8; ++i) {
       const uint4 v = src[i];
-      wv[8 * i + 0] = lo_bf(v.x); wv[8 * i + 1] = hi_bf(v.x);
-      wv[8 * i + 2] = lo_bf(v.y); wv[8 * i + 3] = hi_bf(v.y);
-      wv[8 * i + 4] = lo_bf(v.z); wv[8 * i + 5] = hi_bf(v.z);
-      wv[8 * i + 6] = lo_bf(v.w); wv[8 * i + 7] = hi_bf(v.w);
+      wv[8 * i + 0] = lo_st<F16>(v.x); wv[8 * i + 1] = hi_st<F16>(v.x);
+      wv[8 * i + 2] = lo_st<F16>(v.y); wv[8 * i + 3] = hi_st<F16>(v.y);
+      wv[8 * i + 4] = lo_st<F16>(v.z); wv[8 * i + 5] = hi_st<F16>(v.z);
+      wv[8 * i + 6] = lo_st<F16>(v.w); wv[8 * i + 7] = hi_st<F16>(v.w);
     }
     const float be = bias ? bias[e] : 0.0f;
 #pragma unroll
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
       const int tok = tt * TW + t;
       if (lane == 63 && tok < T) {
         const float v = bias ? s + be : s;
-        logits[(int64_t)tok * E + e] = f2bf(v);
+        logits[(int64_t)tok * E + e] = f2st<F16>(v);
       }
     }
   }
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
 // while the current one is used), each logit exactly as router_logits_kernel
 // computes it. Then wave t ranks token t from the logits in LDS with the same
 // wave-level ranking as topk_kernel.
-template <int C, int ROUTE>
+template <int C, int ROUTE, bool F16>
 __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const float* __restrict__ bias, int T,
@@ -110,10 +110,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
 #pragma unroll
       for (int i = 0; i < C / 8; ++i) {
         const uint4 v = src[i];
-        xv[t][8 * i + 0] = lo_bf(v.x); xv[t][8 * i + 1] = hi_bf(v.x);
-        xv[t][8 * i + 2] = lo_bf(v.y); xv[t][8 * i + 3] = hi_bf(v.y);
-        xv[t][8 * i + 4] = lo_bf(v.z); xv[t][8 * i + 5] = hi_bf(v.z);
-        xv[t][8 * i + 6] = lo_bf(v.w); xv[t][8 * i + 7] = hi_bf(v.w);
+        xv[t][8 * i + 0] = lo_st<F16>(v.x); xv[t][8 * i + 1] = hi_st<F16>(v.x);
+        xv[t][8 * i + 2] = lo_st<F16>(v.y); xv[t][8 * i + 3] = hi_st<F16>(v.y);
+        xv[t][8 * i + 4] = lo_st<F16>(v.z); xv[t][8 * i + 5] = hi_st<F16>(v.z);
+        xv[t][8 * i + 6] = lo_st<F16>(v.w); xv[t][8 * i + 7] = hi_st<F16>(v.w);
       }
     } else {
 #pragma unroll
@@ -129,10 +129,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
     float wv[C];
 #pragma unroll
     for (int i = 0; i < C / 8; ++i) {
-      wv[8 * i + 0] = lo_bf(r[i].x); wv[8 * i + 1] = hi_bf(r[i].x);
-      wv[8 * i + 2] = lo_bf(r[i].y); wv[8 * i + 3] = hi_bf(r[i].y);
-      wv[8 * i + 4] = lo_bf(r[i].z); wv[8 * i + 5] = hi_bf(r[i].z);
-      wv[8 * i + 6] = lo_bf(r[i].w); wv[8 * i + 7] = hi_bf(r[i].w);
+      wv[8 * i + 0] = lo_st<F16>(r[i].x); wv[8 * i + 1] = hi_st<F16>(r[i].x);
+      wv[8 * i + 2] = lo_st<F16>(r[i].y); wv[8 * i + 3] = hi_st<F16>(r[i].y);
+      wv[8 * i + 4] = lo_st<F16>(r[i].z); wv[8 * i + 5] = hi_st<F16>(r[i].z);
+      wv[8 * i + 6] = lo_st<F16>(r[i].w); wv[8 * i + 7] = hi_st<F16>(r[i].w);
     }
     const float be = bias ? bias[e] : 0.0f;
 #pragma unroll
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
 #pragma unroll
       for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
       s = wave_tree_sum64(s);
-      if (lane == 63) s_logit[t][e] = f2bf(bias ? s + be : s);
+      if (lane == 63) s_logit[t][e] = f2st<F16>(bias ? s + be : s);
     }
   };
   const int epw = (E + 3) / 4;
@@ -166,9 +166,9 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
     int id;
     if (ROUTE == TFM_ROUTE_OLMOE) {
       uint16_t gb;
-      id = olmoe_route_wave(row, E, K, &g, &gb);
+      id = olmoe_route_wave<F16>(row, E, K, &g, &gb);
     } else {
-      id = granite_route_wave(row, E, K, &g);
+      id = granite_route_wave<F16>(row, E, K, &g);
     }
     if (lane < K) {
       idx[(int64_t)tok * K + lane] = id;
@@ -180,36 +180,46 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
   if (tid <= E) hist[(int64_t)blockIdx.x * (E + 1) + tid] = h[tid];
 }
 
-template <int C>
+template <int C, bool F16>
 static void launch_router_topk_c(int route_kind, const uint16_t* x, const uint16_t* w,
                                  const float* bias, int T, int H, int E, int K, int32_t* idx,
                                  float* gates_f32, int32_t* hist, uint16_t* logits_out,
                                  hipStream_t s) {
   const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
   if (route_kind == TFM_ROUTE_OLMOE)
-    router_topk_kernel<C, TFM_ROUTE_OLMOE><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                 hist, logits_out);
+    router_topk_kernel<C, TFM_ROUTE_OLMOE, F16><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx,
+                                                                      gates_f32, hist, logits_out);
   else
-    router_topk_kernel<C, TFM_ROUTE_GRANITE><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                   hist, logits_out);
+    router_topk_kernel<C, TFM_ROUTE_GRANITE, F16><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx,
+                                                                        gates_f32, hist, logits_out);
 }
 
-bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
-                        int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
-                        uint16_t* logits_out, hipStream_t s) {
-  if (T <= 0) return true;
+template <bool F16>
+static bool router_topk_dt(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
+                           int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
+                           uint16_t* logits_out, hipStream_t s) {
   switch (H) {
-    case 512: launch_router_topk_c<8>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
-    case 1024: launch_router_topk_c<16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
-    case 1536: launch_router_topk_c<24>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
-    case 2048: launch_router_topk_c<32>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 512: launch_router_topk_c<8, F16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 1024: launch_router_topk_c<16, F16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 1536: launch_router_topk_c<24, F16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
+    case 2048: launch_router_topk_c<32, F16>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s); break;
     default: return false;
   }
-  check_hip(hipGetLastError(), "router_topk launch");
   return true;
 }
 
+bool launch_router_topk(int route_kind, bool f16, const uint16_t* x, const uint16_t* w, const float* bias,
+                        int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
+                        uint16_t* logits_out, hipStream_t s) {
+  if (T <= 0) return true;
+  const bool ok = f16 ? router_topk_dt<true>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s)
+                      : router_topk_dt<false>(route_kind, x, w, bias, T, H, E, K, idx, gates_f32, hist, logits_out, s);
+  if (ok) check_hip(hipGetLastError(), "router_topk launch");
+  return ok;
+}
+
 // Any H % 64 == 0: the same arithmetic with scalar loads.
+template <bool F16>
 __global__ __launch_bounds__(256) void router_logits_generic(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ w,
                                                              const float* __restrict__ bias,
@@ -222,99 +232,111 @@ __global__ __launch_bounds__(256) void router_logits_generic(const uint16_t* __r
   const int c = H / 64;
   float s = 0.0f;
   for (int j = 0; j < c; ++j)
-    s = __builtin_fmaf(bf2f(x[(int64_t)tok * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
+    s = __builtin_fmaf(st2f<F16>(x[(int64_t)tok * H + lane * c + j]), st2f<F16>(w[(int64_t)e * H + lane * c + j]), s);
   s = wave_tree_sum64(s);
-  if (lane == 63) logits[(int64_t)tok * E + e] = f2bf(bias ? s + bias[e] : s);
+  if (lane == 63) logits[(int64_t)tok * E + e] = f2st<F16>(bias ? s + bias[e] : s);
 }
 
-template <int C>
+template <int C, bool F16>
 static void launch_router_c(const uint16_t* x, const uint16_t* w, const float* bias, int T,
                             int H, int E, uint16_t* logits, hipStream_t s) {
   if (T <= 64) {
     // Few tokens: one wave per (token, expert), so the router rows stream in
     // parallel across the chip.
     const int waves = T * E;
-    router_logits_kernel<C, 1><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, 1, logits);
+    router_logits_kernel<C, 1, F16><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, 1, logits);
   } else {
     // Many tokens: a wave keeps 4 token rows in registers and walks 16
     // experts, reading router rows from L2.
     constexpr int TW = 4;
     const int EPW = 16;
     const int waves = ((T + TW - 1) / TW) * ((E + EPW - 1) / EPW);
-    router_logits_kernel<C, TW><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, EPW, logits);
+    router_logits_kernel<C, TW, F16><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, EPW, logits);
   }
 }
 
-void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int T,
-                          int H, int E, uint16_t* logits, hipStream_t s) {
-  if (T <= 0) return;
+template <bool F16>
+static void router_logits_dt(const uint16_t* x, const uint16_t* w, const float* bias, int T,
+                             int H, int E, uint16_t* logits, hipStream_t s) {
   switch (H) {
-    case 512: launch_router_c<8>(x, w, bias, T, H, E, logits, s); break;
-    case 1024: launch_router_c<16>(x, w, bias, T, H, E, logits, s); break;
-    case 1536: launch_router_c<24>(x, w, bias, T, H, E, logits, s); break;
-    case 2048: launch_router_c<32>(x, w, bias, T, H, E, logits, s); break;
+    case 512: launch_router_c<8, F16>(x, w, bias, T, H, E, logits, s); break;
+    case 1024: launch_router_c<16, F16>(x, w, bias, T, H, E, logits, s); break;
+    case 1536: launch_router_c<24, F16>(x, w, bias, T, H, E, logits, s); break;
+    case 2048: launch_router_c<32, F16>(x, w, bias, T, H, E, logits, s); break;
     default: {
       const int64_t waves = (int64_t)T * E;
-      router_logits_generic<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(x, w, bias, T, H, E, logits);
+      router_logits_generic<F16><<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(x, w, bias, T, H, E, logits);
     }
   }
+}
+
+void launch_router_logits(bool f16, const uint16_t* x, const uint16_t* w, const float* bias, int T,
+                          int H, int E, uint16_t* logits, hipStream_t s) {
+  if (T <= 0) return;
+  if (f16)
+    router_logits_dt<true>(x, w, bias, T, H, E, logits, s);
+  else
+    router_logits_dt<false>(x, w, bias, T, H, E, logits, s);
   check_hip(hipGetLastError(), "router_logits launch");
 }
 
 // Affine-quantised router (native_affine_qmm of the router weight,
-// export_native_olmoe_target.py:194-200): the dense router's arithmetic with
-// w[e,h] = st(fmaf(s, q, b)), the dequantised weight rounded to the storage
-// dtype (native_affine_ops.py:29-36). One wave per (token, expert); x and the
-// logits are in the storage dtype (bf16, or half when F16), scales and biases
-// too. Group size 64.
+// export_native_olmoe_target.py:194-200) dequantised once per call into a
+// dense [E, H] matrix in the storage dtype: w[e,h] = st(fmaf(s, q, b)), the
+// value native_affine_ops.py:29-36 rounds to the scales' dtype. The dense
+// router kernels then compute the logits in their bit-defined order. One
+// thread per packed word (8 or 4 codes); group size 64.
 template <bool F16, int BITS>
-__global__ __launch_bounds__(256) void affine_router_logits_kernel(const uint16_t* __restrict__ x,
-                                                                   const uint32_t* __restrict__ q,
-                                                                   const uint16_t* __restrict__ sc,
-                                                                   const uint16_t* __restrict__ bi,
-                                                                   const float* __restrict__ bias,
-                                                                   int T, int H, int E,
-                                                                   uint16_t* __restrict__ logits) {
+__global__ __launch_bounds__(256) void dequant_router_kernel(const uint32_t* __restrict__ q,
+                                                             const uint16_t* __restrict__ sc,
+                                                             const uint16_t* __restrict__ bi,
+                                                             int64_t words, int H,
+                                                             uint16_t* __restrict__ w) {
   constexpr int PER = 32 / BITS;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wave >= (int64_t)T * E) return;  // whole wave exits together
-  const int tok = (int)(wave / E), e = (int)(wave % E);
-  const int c = H / 64;
-  const uint16_t* xr = x + (int64_t)tok * H;
-  const uint32_t* qr = q + (int64_t)e * (H / PER);
-  const uint16_t* sr = sc + (int64_t)e * (H / 64);
-  const uint16_t* br = bi + (int64_t)e * (H / 64);
-  float acc = 0.0f;
-  for (int j = 0; j < c; ++j) {
-    const int k = lane * c + j;
-    const uint32_t code = (qr[k / PER] >> (BITS * (k % PER))) & MASK;
-    const float wv = st2f<F16>(f2st<F16>(__builtin_fmaf(st2f<F16>(sr[k >> 6]), (float)code, st2f<F16>(br[k >> 6]))));
-    acc = __builtin_fmaf(st2f<F16>(xr[k]), wv, acc);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int64_t k0 = i * PER;               // first element: row k0 / H, column k0 % H
+  const int64_t g = k0 / 64;                // rows are whole groups (H % 64 == 0)
+  const float s = st2f<F16>(sc[g]), b = st2f<F16>(bi[g]);
+  const uint32_t word = q[i];
+  uint16_t out[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    out[j] = f2st<F16>(__builtin_fmaf(s, (float)((word >> (BITS * j)) & MASK), b));
+  if constexpr (PER == 8) {
+    uint4 v;
+    v.x = out[0] | ((uint32_t)out[1] << 16);
+    v.y = out[2] | ((uint32_t)out[3] << 16);
+    v.z = out[4] | ((uint32_t)out[5] << 16);
+    v.w = out[6] | ((uint32_t)out[7] << 16);
+    *reinterpret_cast<uint4*>(w + k0) = v;
+  } else {
+    uint2 v;
+    v.x = out[0] | ((uint32_t)out[1] << 16);
+    v.y = out[2] | ((uint32_t)out[3] << 16);
+    *reinterpret_cast<uint2*>(w + k0) = v;
   }
-  acc = wave_tree_sum64(acc);
-  if (lane == 63) logits[(int64_t)tok * E + e] = f2st<F16>(bias ? acc + bias[e] : acc);
+  (void)H;
 }
 
-void launch_affine_router_logits(bool f16, int bits, const uint16_t* x, const tfm_affine& w,
-                                 const float* bias, int T, int H, int E, uint16_t* logits,
-                                 hipStream_t s) {
-  if (T <= 0) return;
-  const int64_t waves = (int64_t)T * E;
-  const unsigned blocks = (unsigned)((waves + 3) / 4);
-  const uint32_t* q = static_cast<const uint32_t*>(w.q);
-  const uint16_t* sc = static_cast<const uint16_t*>(w.scales);
-  const uint16_t* bi = static_cast<const uint16_t*>(w.biases);
+void launch_dequant_router(bool f16, int bits, const tfm_affine& r, int E, int H, uint16_t* w,
+                           hipStream_t s) {
+  const int64_t words = (int64_t)E * H * bits / 32;
+  if (words <= 0) return;
+  const unsigned blocks = (unsigned)((words + 255) / 256);
+  const uint32_t* q = static_cast<const uint32_t*>(r.q);
+  const uint16_t* sc = static_cast<const uint16_t*>(r.scales);
+  const uint16_t* bi = static_cast<const uint16_t*>(r.biases);
   if (f16 && bits == 8)
-    affine_router_logits_kernel<true, 8><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+    dequant_router_kernel<true, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
   else if (f16)
-    affine_router_logits_kernel<true, 4><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+    dequant_router_kernel<true, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
   else if (bits == 8)
-    affine_router_logits_kernel<false, 8><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
+    dequant_router_kernel<false, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
   else
-    affine_router_logits_kernel<false, 4><<<blocks, 256, 0, s>>>(x, q, sc, bi, bias, T, H, E, logits);
-  check_hip(hipGetLastError(), "affine router launch");
+    dequant_router_kernel<false, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
+  check_hip(hipGetLastError(), "router dequant launch");
 }
 
 __device__ __forceinline__ float readlane_f(float v, int j) {

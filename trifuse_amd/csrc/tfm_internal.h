@@ -59,7 +59,7 @@ struct Grouping {
 };
 
 // ---- launchers (defined in the .hip files) ----
-void launch_router_logits(const uint16_t* x, const uint16_t* w, const float* bias, int T,
+void launch_router_logits(bool f16, const uint16_t* x, const uint16_t* w, const float* bias, int T,
                           int H, int E, uint16_t* logits, hipStream_t s);
 // f16: logits/values/probabilities are IEEE half bits instead of bf16.
 void launch_topk(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,
@@ -67,11 +67,10 @@ void launch_topk(int route_kind, bool f16, const uint16_t* logits, int T, int E,
 void launch_rank_topk(int rule, bool f16, const uint16_t* values, int T, int n, int K, int32_t* idx,
                       hipStream_t s);
 void launch_olmoe_softmax(bool f16, const uint16_t* logits, int T, int E, uint16_t* probs, hipStream_t s);
-// Affine-quantised router [E, H] (bits 4 or 8, group 64): logits in the
-// storage dtype with the dense router's bit-defined order.
-void launch_affine_router_logits(bool f16, int bits, const uint16_t* x, const tfm_affine& w,
-                                 const float* bias, int T, int H, int E, uint16_t* logits,
-                                 hipStream_t s);
+// Affine-quantised router [E, H] (bits 4 or 8, group 64) dequantised into a
+// dense [E, H] matrix w in the storage dtype, for the dense router kernels.
+void launch_dequant_router(bool f16, int bits, const tfm_affine& r, int E, int H, uint16_t* w,
+                           hipStream_t s);
 // Grouping (group.hip): per-chunk expert histograms, then a stable scatter.
 // hist holds group_blocks(n, chunk) rows of E+1 counts (bucket E: bad ids).
 constexpr int kGroupChunk = 512;           // routes per chunk for given routes
@@ -89,7 +88,7 @@ void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, int32
 // Prefill routing in one kernel: logits (optionally written out), top-k and
 // the chunk histogram of kTopkTokensPerBlock tokens per chunk. Returns false
 // (nothing launched) for a hidden size it has no variant for.
-bool launch_router_topk(int route_kind, const uint16_t* x, const uint16_t* w, const float* bias,
+bool launch_router_topk(int route_kind, bool f16, const uint16_t* x, const uint16_t* w, const float* bias,
                         int T, int H, int E, int K, int32_t* idx, float* gates_f32, int32_t* hist,
                         uint16_t* logits_out, hipStream_t s);
 void launch_topk_hist(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,

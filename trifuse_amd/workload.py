@@ -43,9 +43,13 @@ class Geometry:
 
     @property
     def expert_bytes(self) -> int:
-        """Packed Q + bf16 scales + bf16 biases of one expert (gate, up, down)."""
+        """Packed 4-bit Q + 16-bit scales + biases of one expert (gate, up, down)."""
+        return self.expert_bytes_at(4)
+
+    def expert_bytes_at(self, bits: int) -> int:
+        """Packed Q at `bits` + 16-bit scales + biases of one expert (gate, up, down)."""
         H, I = self.hidden, self.intermediate
-        q = 3 * H * I // 2
+        q = 3 * H * I * bits // 8
         sb = 3 * 2 * (H * I // GROUP) * 2
         return q + sb
 
@@ -62,6 +66,13 @@ class Workload:
     layers: int = 1
     zipf: bool = False
     description: str = ""
+    bits: int = 4                # expert code width
+    dtype: str = "bf16"          # activation / scale storage: "bf16" or "f16"
+    router: str = "dense"        # "dense" bf16 router or "affine" 4-bit router
+
+    @property
+    def torch_dtype(self):
+        return torch.float16 if self.dtype == "f16" else torch.bfloat16
 
 
 WORKLOADS: Dict[str, Workload] = {
@@ -77,6 +88,18 @@ WORKLOADS: Dict[str, Workload] = {
                                       description="Granite-3.0-3B-A800M MoE block, prefill 2048 tokens"),
     "granite_decode_t32": Workload("granite_decode_t32", GRANITE, 32, 1,
                                    description="Granite-3.0-3B-A800M MoE block, decode batch 32"),
+    "olmoe_decode_t8_x16_int8": Workload("olmoe_decode_t8_x16_int8", OLMOE, 8, 16, bits=8,
+                                         description="OLMoE MoE block, decode batch 8, 8-bit experts"),
+    "olmoe_prefill_t512_int8": Workload("olmoe_prefill_t512_int8", OLMOE, 512, 1, bits=8,
+                                        description="OLMoE MoE block, prefill 512 tokens, 8-bit experts"),
+    "olmoe_decode_t8_x16_f16": Workload("olmoe_decode_t8_x16_f16", OLMOE, 8, 16, dtype="f16",
+                                        router="affine",
+                                        description="OLMoE MoE block, decode batch 8, f16 packs with "
+                                                    "the affine 4-bit router"),
+    "olmoe_prefill_t512_f16": Workload("olmoe_prefill_t512_f16", OLMOE, 512, 1, dtype="f16",
+                                       router="affine",
+                                       description="OLMoE MoE block, prefill 512 tokens, f16 packs with "
+                                                   "the affine 4-bit router"),
 }
 
 
@@ -216,7 +239,8 @@ def workload_layers(wl: Workload, device="cpu", layers: Optional[int] = None) ->
     layer count). The two Granite workloads share weights (prefill then decode)."""
     tag = "shared" if wl.geometry is GRANITE else wl.name
     n = wl.layers if layers is None else layers
-    return [make_layer(wl.geometry, l, device, zipf=wl.zipf, seed_tag=tag) for l in range(n)]
+    return [make_layer(wl.geometry, l, device, zipf=wl.zipf, seed_tag=tag, bits=wl.bits,
+                       dtype=wl.torch_dtype, affine_router=wl.router == "affine") for l in range(n)]
 
 
 # Distinct layers a timing loop rotates through: 16 layers of either geometry
@@ -226,14 +250,17 @@ TIMING_LAYERS = 16
 
 
 def workload_x(wl: Workload) -> torch.Tensor:
-    return make_x(wl.geometry, wl.tokens, tag=wl.name)
+    return make_x(wl.geometry, wl.tokens, tag=wl.name, dtype=wl.torch_dtype)
 
 
-def algorithmic_bytes(geom: Geometry, tokens: int, distinct_experts: int) -> int:
+def algorithmic_bytes(geom: Geometry, tokens: int, distinct_experts: int, bits: int = 4,
+                      affine_router: bool = False) -> int:
     """HBM bytes one MoE layer must move: routed experts' packed weights,
-    the router, the activations in and the result out."""
-    return (distinct_experts * geom.expert_bytes + geom.experts * geom.hidden * 2
-            + 2 * tokens * geom.hidden * 2)
+    the router (dense 16-bit, or 4-bit codes plus 16-bit scales and biases),
+    the activations in and the result out."""
+    E, H = geom.experts, geom.hidden
+    router = E * H // 2 + 2 * (E * H // GROUP) * 2 if affine_router else E * H * 2
+    return distinct_experts * geom.expert_bytes_at(bits) + router + 2 * tokens * H * 2
 
 
 def algorithmic_flops(geom: Geometry, tokens: int) -> int:
