@@ -139,3 +139,26 @@ def test_forward_rmsnorm_f16(gpu):
     sample = _sample(48, 12)
     ref = oracle.moe_reference(post, ridx, rg, lay, tokens=sample, residual=u16(h), rm=0.25, dtype="f16")
     assert max_rel(oracle.st_to_f32(u16(y), "f16")[sample], ref) <= BLOCK_TOL
+
+
+def test_f16_decode_paths_agree(gpu):
+    # At decode shapes half blocks take the streaming kernels: the hook (given
+    # routes) matches the whole block bit for bit, and one or two tokens (the
+    # fused down + combine) match the same tokens inside a three-token batch.
+    geom = wl.OLMOE
+    log("f16 decode hook / small-batch agreement")
+    gpu_dev = torch.device("cuda:0")
+    layer = wl.make_layer(geom, 3, gpu_dev, seed_tag="f16dec", dtype=F16, affine_router=True)
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    blk = _block(geom, rm=0.5)
+    x = wl.make_x(geom, 8, tag="f16dec_x", dtype=F16).to(gpu_dev)
+    res = wl.make_x(geom, 8, tag="f16dec_r", dtype=F16).to(gpu_dev)
+    y8, idx, gates = blk.forward(x, wts, residual=res, return_routes=True)
+    y8h = blk.experts(x, idx, gates, wts, residual=res)
+    y3 = blk.forward(x[:3].contiguous(), wts, residual=res[:3].contiguous())
+    y2 = blk.forward(x[:2].contiguous(), wts, residual=res[:2].contiguous())
+    y1 = blk.forward(x[:1].contiguous(), wts, residual=res[:1].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(y8, y8h)
+    assert torch.equal(y2, y3[:2]) and torch.equal(y1, y3[:1])
+    assert torch.equal(y3, y8[:3])

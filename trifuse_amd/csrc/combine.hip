@@ -16,7 +16,7 @@ namespace tfm {
 // then every row is requested before the first is used (rows of bad routes
 // read row 0 and are dropped by a select), so a thread waits for memory
 // twice rather than twice per route; larger K takes the plain loop.
-template <int KMAX>
+template <int KMAX, bool F16>
 __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __restrict__ P,
                                                              const int32_t* __restrict__ inverse,
                                                              const int32_t* __restrict__ n_valid,
@@ -64,8 +64,8 @@ __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __rest
   float r[8];
   if (residual) {
     const uint4 rv = *reinterpret_cast<const uint4*>(residual + (int64_t)t * H + c);
-    r[0] = lo_bf(rv.x); r[1] = hi_bf(rv.x); r[2] = lo_bf(rv.y); r[3] = hi_bf(rv.y);
-    r[4] = lo_bf(rv.z); r[5] = hi_bf(rv.z); r[6] = lo_bf(rv.w); r[7] = hi_bf(rv.w);
+    r[0] = lo_st<F16>(rv.x); r[1] = hi_st<F16>(rv.x); r[2] = lo_st<F16>(rv.y); r[3] = hi_st<F16>(rv.y);
+    r[4] = lo_st<F16>(rv.z); r[5] = hi_st<F16>(rv.z); r[6] = lo_st<F16>(rv.w); r[7] = hi_st<F16>(rv.w);
   } else {
 #pragma unroll
     for (int v = 0; v < 8; ++v) r[v] = 0.0f;
@@ -73,20 +73,23 @@ __global__ __launch_bounds__(256) void combine_sorted_kernel(const float* __rest
   // y = bf16(fma(rm, sum, residual)), the rounding the fused small-batch
   // decode kernel (dstream.hip) reproduces.
   uint4 o;
-  o.x = pack_bf16x2(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
-  o.y = pack_bf16x2(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
-  o.z = pack_bf16x2(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
-  o.w = pack_bf16x2(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
+  o.x = pack_st2<F16>(__builtin_fmaf(rmul, s[0], r[0]), __builtin_fmaf(rmul, s[1], r[1]));
+  o.y = pack_st2<F16>(__builtin_fmaf(rmul, s[2], r[2]), __builtin_fmaf(rmul, s[3], r[3]));
+  o.z = pack_st2<F16>(__builtin_fmaf(rmul, s[4], r[4]), __builtin_fmaf(rmul, s[5], r[5]));
+  o.w = pack_st2<F16>(__builtin_fmaf(rmul, s[6], r[6]), __builtin_fmaf(rmul, s[7], r[7]));
   *reinterpret_cast<uint4*>(y + (int64_t)t * H + c) = o;
 }
 
-void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
+void launch_combine_sorted(bool f16, const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
                            int K, int H, const uint16_t* residual, float rmul, uint16_t* y,
                            hipStream_t s) {
   if (T <= 0) return;
   const int64_t n = (int64_t)T * (H / 8);
-  combine_sorted_kernel<8><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, inverse, n_valid, T, K, H,
-                                                                      residual, rmul, y);
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  if (f16)
+    combine_sorted_kernel<8, true><<<blocks, 256, 0, s>>>(P, inverse, n_valid, T, K, H, residual, rmul, y);
+  else
+    combine_sorted_kernel<8, false><<<blocks, 256, 0, s>>>(P, inverse, n_valid, T, K, H, residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
 // over E compute units (a single compute unit pulling the whole router is
 // limited by its own outstanding misses). Wave w takes tokens w, w + 4, ..,
 // two at a time.
-template <int C>
+template <int C, bool F16>
 __global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
                                                             const float* __restrict__ bias, int T,
@@ -160,10 +160,10 @@ __global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __re
 #pragma unroll
   for (int i = 0; i < C / 8; ++i) {
     const uint4 v = ws[i];
-    wv[8 * i + 0] = lo_bf(v.x); wv[8 * i + 1] = hi_bf(v.x);
-    wv[8 * i + 2] = lo_bf(v.y); wv[8 * i + 3] = hi_bf(v.y);
-    wv[8 * i + 4] = lo_bf(v.z); wv[8 * i + 5] = hi_bf(v.z);
-    wv[8 * i + 6] = lo_bf(v.w); wv[8 * i + 7] = hi_bf(v.w);
+    wv[8 * i + 0] = lo_st<F16>(v.x); wv[8 * i + 1] = hi_st<F16>(v.x);
+    wv[8 * i + 2] = lo_st<F16>(v.y); wv[8 * i + 3] = hi_st<F16>(v.y);
+    wv[8 * i + 4] = lo_st<F16>(v.z); wv[8 * i + 5] = hi_st<F16>(v.z);
+    wv[8 * i + 6] = lo_st<F16>(v.w); wv[8 * i + 7] = hi_st<F16>(v.w);
   }
   const float be = bias ? bias[e] : 0.0f;
   // Token rows past T read zeros (offset beyond the buffer).
@@ -187,23 +187,24 @@ __global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __re
 #pragma unroll
         for (int i = 0; i < C / 8; ++i) {
           const uint4 v = xv[u][i];
-          s = __builtin_fmaf(lo_bf(v.x), wv[8 * i + 0], s);
-          s = __builtin_fmaf(hi_bf(v.x), wv[8 * i + 1], s);
-          s = __builtin_fmaf(lo_bf(v.y), wv[8 * i + 2], s);
-          s = __builtin_fmaf(hi_bf(v.y), wv[8 * i + 3], s);
-          s = __builtin_fmaf(lo_bf(v.z), wv[8 * i + 4], s);
-          s = __builtin_fmaf(hi_bf(v.z), wv[8 * i + 5], s);
-          s = __builtin_fmaf(lo_bf(v.w), wv[8 * i + 6], s);
-          s = __builtin_fmaf(hi_bf(v.w), wv[8 * i + 7], s);
+          s = __builtin_fmaf(lo_st<F16>(v.x), wv[8 * i + 0], s);
+          s = __builtin_fmaf(hi_st<F16>(v.x), wv[8 * i + 1], s);
+          s = __builtin_fmaf(lo_st<F16>(v.y), wv[8 * i + 2], s);
+          s = __builtin_fmaf(hi_st<F16>(v.y), wv[8 * i + 3], s);
+          s = __builtin_fmaf(lo_st<F16>(v.z), wv[8 * i + 4], s);
+          s = __builtin_fmaf(hi_st<F16>(v.z), wv[8 * i + 5], s);
+          s = __builtin_fmaf(lo_st<F16>(v.w), wv[8 * i + 6], s);
+          s = __builtin_fmaf(hi_st<F16>(v.w), wv[8 * i + 7], s);
         }
         s = wave_tree_sum64(s);
-        if (lane == 63) logits[(int64_t)t * E + e] = f2bf(bias ? s + be : s);
+        if (lane == 63) logits[(int64_t)t * E + e] = f2st<F16>(bias ? s + be : s);
       }
     }
   }
 }
 
 // Any H % 64 == 0: the same arithmetic as decode_logits_kernel with scalar loads.
+template <bool F16>
 __global__ __launch_bounds__(256) void decode_logits_generic(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ w,
                                                              const float* __restrict__ bias, int T,
@@ -216,9 +217,9 @@ __global__ __launch_bounds__(256) void decode_logits_generic(const uint16_t* __r
   for (int t = wave; t < T; t += 4) {
     float s = 0.0f;
     for (int j = 0; j < c; ++j)
-      s = __builtin_fmaf(bf2f(x[(int64_t)t * H + lane * c + j]), bf2f(w[(int64_t)e * H + lane * c + j]), s);
+      s = __builtin_fmaf(st2f<F16>(x[(int64_t)t * H + lane * c + j]), st2f<F16>(w[(int64_t)e * H + lane * c + j]), s);
     s = wave_tree_sum64(s);
-    if (lane == 63) logits[(int64_t)t * E + e] = f2bf(bias ? s + bias[e] : s);
+    if (lane == 63) logits[(int64_t)t * E + e] = f2st<F16>(bias ? s + bias[e] : s);
   }
 }
 
@@ -227,18 +228,27 @@ static int lg_for(int kin) {
   return nch <= 4 ? 4 : nch <= 8 ? 8 : nch <= 16 ? 16 : nch <= 32 ? 32 : 64;
 }
 
-void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
-                          int E, uint16_t* logits, hipStream_t s) {
+template <bool F16>
+static void decode_logits_dt(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
+                             int E, uint16_t* logits, hipStream_t s) {
+  switch (H) {
+    case 512: decode_logits_kernel<8, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1024: decode_logits_kernel<16, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 1536: decode_logits_kernel<24, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 2048: decode_logits_kernel<32, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    default: decode_logits_generic<F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+  }
+}
+
+void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, const float* bias, int T,
+                          int H, int E, uint16_t* logits, hipStream_t s) {
   if (T <= 0) return;
   if (E > 64) fail(TFM_E_UNSUPPORTED, "decode routing: more than 64 experts");
   if (!logits) fail(TFM_E_INVALID, "decode routing: logits buffer missing");
-  switch (H) {
-    case 512: decode_logits_kernel<8><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1024: decode_logits_kernel<16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1536: decode_logits_kernel<24><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 2048: decode_logits_kernel<32><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    default: decode_logits_generic<<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-  }
+  if (f16)
+    decode_logits_dt<true>(x, router, bias, T, H, E, logits, s);
+  else
+    decode_logits_dt<false>(x, router, bias, T, H, E, logits, s);
   check_hip(hipGetLastError(), "decode logits launch");
 }
 
@@ -246,16 +256,7 @@ void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* rout
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s) {
   if (T <= 0) return;
-  if (E > 64) fail(TFM_E_UNSUPPORTED, "decode routing: more than 64 experts");
-  if (!logits) fail(TFM_E_INVALID, "decode routing: logits buffer missing");
-  switch (H) {
-    case 512: decode_logits_kernel<8><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1024: decode_logits_kernel<16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1536: decode_logits_kernel<24><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 2048: decode_logits_kernel<32><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    default: decode_logits_generic<<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-  }
-  check_hip(hipGetLastError(), "decode logits launch");
+  launch_decode_logits(false, x, router, bias, T, H, E, logits, s);
   launch_topk(route_kind, false, logits, T, E, K, idx, nullptr, gates, s);
 }
 

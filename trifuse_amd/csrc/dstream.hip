@@ -32,7 +32,23 @@
 #include "gemv_body.h"
 #include "route_wave.h"
 
+// Compiled twice: as is for bf16 storage (namespace tfm::ds_bf16) and from
+// dstream_f16.hip for IEEE-half storage (tfm::ds_f16). Only the arithmetic on
+// 16-bit values differs: conversions, the dot2 instruction, the exponent
+// byte of the unpacked codes and the matching code base.
+#ifndef TFM_DS_F16
+#define TFM_DS_F16 0
+#endif
+#if TFM_DS_F16
+#define TFM_DS_NS ds_f16
+#else
+#define TFM_DS_NS ds_bf16
+#endif
+
 namespace tfm {
+namespace TFM_DS_NS {
+
+constexpr bool kF16 = TFM_DS_F16 != 0;
 
 constexpr int kDsCostUnpack = 2;  // item cost = kDsCostUnpack + routes of its expert
 constexpr int kDsSmallT = 2;      // tokens up to which the three-kernel layer is used
@@ -146,9 +162,9 @@ __device__ __forceinline__ void ds_rank_group(DsGroupLds& L, const uint16_t* __r
       int id;
       if (MODE == TFM_ROUTE_OLMOE) {
         uint16_t gb;
-        id = olmoe_route_wave(row, E, K, &gv, &gb);
+        id = olmoe_route_wave<kF16>(row, E, K, &gv, &gb);
       } else {
-        id = granite_route_wave(row, E, K, &gv);
+        id = granite_route_wave<kF16>(row, E, K, &gv);
       }
       if (lane < K) {
         L.e[t * K + lane] = id;
@@ -272,7 +288,7 @@ constexpr int kDsXChunks = 4;  // most x chunks staged per thread by the gate/up
 // xs[(slot*4 + q)*nch + k], and its sum in xsum[slot*nch + k].
 __device__ __forceinline__ void ds_store_chunk(const uint4 (&r)[4], uint4* xs, float* xsum, int slot, int k,
                                                int nch) {
-  const uint32_t ones = 0x3f803f80u;  // (1.0, 1.0) in bf16
+  const uint32_t ones = ones2(kF16);  // (1.0, 1.0) in the storage dtype
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -281,10 +297,10 @@ __device__ __forceinline__ void ds_store_chunk(const uint4 (&r)[4], uint4* xs, f
                                               __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
                                               __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
                                               __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
-    sum = dot2(v.x, ones, sum);
-    sum = dot2(v.y, ones, sum);
-    sum = dot2(v.z, ones, sum);
-    sum = dot2(v.w, ones, sum);
+    sum = dot2_st<kF16>(v.x, ones, sum);
+    sum = dot2_st<kF16>(v.y, ones, sum);
+    sum = dot2_st<kF16>(v.z, ones, sum);
+    sum = dot2_st<kF16>(v.w, ones, sum);
   }
   xsum[slot * nch + k] = sum;
 }
@@ -293,7 +309,7 @@ __device__ __forceinline__ void ds_store_chunk(const uint4 (&r)[4], uint4* xs, f
 __device__ __forceinline__ void ds_stage_chunk(const uint16_t* __restrict__ src, uint4* xs, float* xsum,
                                                int slot, int k, int nch) {
   ChunkX cx;
-  load_x(src, cx);
+  load_x<kF16>(src, cx);
 #pragma unroll
   for (int q = 0; q < 4; ++q)
     xs[(slot * 4 + q) * nch + k] = make_uint4(cx.p[4 * q], cx.p[4 * q + 1], cx.p[4 * q + 2], cx.p[4 * q + 3]);
@@ -338,9 +354,9 @@ __device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restr
 #pragma unroll
     for (int q = 0; q < 4; ++q) v[q] = xs[(tok * 4 + q) * nch + k];
     const float xsm = xsum[tok * nch + k];
-    const float sg = bf2f((uint16_t)w.g[c].s), su = bf2f((uint16_t)w.u[c].s);
-    const float cg = __builtin_fmaf(-128.0f, sg, bf2f((uint16_t)w.g[c].b));
-    const float cu = __builtin_fmaf(-128.0f, su, bf2f((uint16_t)w.u[c].b));
+    const float sg = st2f<kF16>((uint16_t)w.g[c].s), su = st2f<kF16>((uint16_t)w.u[c].s);
+    const float cg = __builtin_fmaf(-code_base(kF16), sg, st2f<kF16>((uint16_t)w.g[c].b));
+    const float cu = __builtin_fmaf(-code_base(kF16), su, st2f<kF16>((uint16_t)w.u[c].b));
     float dg = 0.0f, du = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -349,16 +365,16 @@ __device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restr
       uint32_t wg = word_of(w.g[c].q, q), wu = word_of(w.u[c].q, q);
       asm volatile("" : "+v"(wg), "+v"(wu));
       uint32_t pg[4], pu[4];
-      unpack_word(wg, pg);
-      unpack_word(wu, pu);
-      dg = dot2(pg[0], v[q].x, dg);
-      du = dot2(pu[0], v[q].x, du);
-      dg = dot2(pg[1], v[q].y, dg);
-      du = dot2(pu[1], v[q].y, du);
-      dg = dot2(pg[2], v[q].z, dg);
-      du = dot2(pu[2], v[q].z, du);
-      dg = dot2(pg[3], v[q].w, dg);
-      du = dot2(pu[3], v[q].w, du);
+      unpack_word_st<kF16>(wg, pg);
+      unpack_word_st<kF16>(wu, pu);
+      dg = dot2_st<kF16>(pg[0], v[q].x, dg);
+      du = dot2_st<kF16>(pu[0], v[q].x, du);
+      dg = dot2_st<kF16>(pg[1], v[q].y, dg);
+      du = dot2_st<kF16>(pu[1], v[q].y, du);
+      dg = dot2_st<kF16>(pg[2], v[q].z, dg);
+      du = dot2_st<kF16>(pu[2], v[q].z, du);
+      dg = dot2_st<kF16>(pg[3], v[q].w, dg);
+      du = dot2_st<kF16>(pu[3], v[q].w, du);
     }
     ag += __builtin_fmaf(sg, dg, cg * xsm);
     au += __builtin_fmaf(su, du, cu * xsm);
@@ -440,7 +456,7 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     const float up = dpp_group_sum<16>(au);
     if (ll == 0 && n < N) {
       const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
-      A.h[(int64_t)j * N + n] = f2bf(hv);
+      A.h[(int64_t)j * N + n] = f2st<kF16>(hv);
     }
   };
   // Routes one at a time through one branch-free body (the nibble unpack is
@@ -512,16 +528,16 @@ __device__ __forceinline__ void ds_dn_dot(const DsDn<C, RG>& w, const uint4* __r
         uint32_t wq = word_of(w.r[g][c].q, q);
         asm volatile("" : "+v"(wq));  // keeps the unpack inside the route loop
         uint32_t p[4];
-        unpack_word(wq, p);
-        d[g] = dot2(p[0], v[q].x, d[g]);
-        d[g] = dot2(p[1], v[q].y, d[g]);
-        d[g] = dot2(p[2], v[q].z, d[g]);
-        d[g] = dot2(p[3], v[q].w, d[g]);
+        unpack_word_st<kF16>(wq, p);
+        d[g] = dot2_st<kF16>(p[0], v[q].x, d[g]);
+        d[g] = dot2_st<kF16>(p[1], v[q].y, d[g]);
+        d[g] = dot2_st<kF16>(p[2], v[q].z, d[g]);
+        d[g] = dot2_st<kF16>(p[3], v[q].w, d[g]);
       }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
-      const float sc = bf2f((uint16_t)w.r[g][c].s);
-      const float cc = __builtin_fmaf(-128.0f, sc, bf2f((uint16_t)w.r[g][c].b));
+      const float sc = st2f<kF16>((uint16_t)w.r[g][c].s);
+      const float cc = __builtin_fmaf(-code_base(kF16), sc, st2f<kF16>((uint16_t)w.r[g][c].b));
       acc[g] += __builtin_fmaf(sc, d[g], cc * xsm);
     }
   }
@@ -690,8 +706,8 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
         const int e = A.idx[f];
         if (e >= 0 && e < E) sacc = __fadd_rn(sacc, s_p[f][rsub]);
       }
-      const float r = A.residual ? bf2f(A.residual[(int64_t)t * N + n]) : 0.0f;
-      A.y[(int64_t)t * N + n] = (uint16_t)pack_bf16x2(__builtin_fmaf(A.rmul, sacc, r), 0.0f);
+      const float r = A.residual ? st2f<kF16>(A.residual[(int64_t)t * N + n]) : 0.0f;
+      A.y[(int64_t)t * N + n] = (uint16_t)pack_st2<kF16>(__builtin_fmaf(A.rmul, sacc, r), 0.0f);
     }
   }
 }
@@ -892,4 +908,5 @@ void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const f
   check_hip(hipGetLastError(), "decode down+combine launch");
 }
 
+}  // namespace TFM_DS_NS
 }  // namespace tfm

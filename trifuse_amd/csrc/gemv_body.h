@@ -17,6 +17,23 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+// The same dot product on packed pairs of the storage dtype: bf16 pairs, or
+// IEEE-half pairs (v_dot2_f32_f16) when F16.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <bool F16>
+__device__ __forceinline__ float dot2_st(uint32_t a, uint32_t b, float c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+  else
+    return dot2(a, b, c);
+}
+
+// (1.0, 1.0) in the storage dtype, and the value of the exponent byte that
+// unpack_word_st places above each code: a code q becomes base + q exactly
+// (bf16 0x43qq = 128 + q, half 0x64qq = 1024 + q for q < 16).
+__host__ __device__ constexpr uint32_t ones2(bool f16) { return f16 ? 0x3c003c00u : 0x3f803f80u; }
+__host__ __device__ constexpr float code_base(bool f16) { return f16 ? 1024.0f : 128.0f; }
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
   const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
@@ -31,9 +48,10 @@ struct ChunkX {
   float sum;
 };
 
+template <bool F16 = false>
 __device__ __forceinline__ void load_x(const uint16_t* __restrict__ src, ChunkX& cx) {
   const uint4* p4 = reinterpret_cast<const uint4*>(src);
-  const uint32_t ones = 0x3f803f80u;  // (1.0, 1.0) in bf16
+  const uint32_t ones = ones2(F16);  // (1.0, 1.0) in the storage dtype
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -42,10 +60,10 @@ __device__ __forceinline__ void load_x(const uint16_t* __restrict__ src, ChunkX&
     cx.p[4 * i + 1] = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);  // (x4, x6)
     cx.p[4 * i + 2] = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);  // (x1, x3)
     cx.p[4 * i + 3] = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);  // (x5, x7)
-    sum = dot2(v.x, ones, sum);
-    sum = dot2(v.y, ones, sum);
-    sum = dot2(v.z, ones, sum);
-    sum = dot2(v.w, ones, sum);
+    sum = dot2_st<F16>(v.x, ones, sum);
+    sum = dot2_st<F16>(v.y, ones, sum);
+    sum = dot2_st<F16>(v.z, ones, sum);
+    sum = dot2_st<F16>(v.w, ones, sum);
   }
   cx.sum = sum;
 }
@@ -54,6 +72,17 @@ __device__ __forceinline__ void load_x(const uint16_t* __restrict__ src, ChunkX&
 // v_perm_b32 picks the nibble bytes of lo/hi and the 0x43 exponent bytes.
 __device__ __forceinline__ void unpack_word(uint32_t w, uint32_t* q) {
   const uint32_t magic = 0x43434343u;
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  q[0] = __builtin_amdgcn_perm(magic, lo, 0x04010400u);
+  q[1] = __builtin_amdgcn_perm(magic, lo, 0x04030402u);
+  q[2] = __builtin_amdgcn_perm(magic, hi, 0x04010400u);
+  q[3] = __builtin_amdgcn_perm(magic, hi, 0x04030402u);
+}
+
+// unpack_word for the storage dtype: pairs of (base+q) in bf16 or half.
+template <bool F16>
+__device__ __forceinline__ void unpack_word_st(uint32_t w, uint32_t* q) {
+  const uint32_t magic = F16 ? 0x64646464u : 0x43434343u;
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
   q[0] = __builtin_amdgcn_perm(magic, lo, 0x04010400u);
   q[1] = __builtin_amdgcn_perm(magic, lo, 0x04030402u);

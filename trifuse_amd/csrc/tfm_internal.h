@@ -103,8 +103,8 @@ void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, i
 void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s);
-void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
-                          int E, uint16_t* logits, hipStream_t s);
+void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, const float* bias, int T,
+                          int H, int E, uint16_t* logits, hipStream_t s);
 
 // Streaming decode path (dstream.hip). decode_stream_fits: the shapes it
 // has variants for. ds_gateup routes (mode TFM_ROUTE_OLMOE/GRANITE: ranks
@@ -112,21 +112,53 @@ void launch_decode_logits(const uint16_t* x, const uint16_t* router, const float
 // kDsGivenRoutes: reads idx/gates), groups them, publishes the grouping
 // (g with g.slots and g.gates_sorted) and the status word, and writes the
 // SwiGLU rows h in sorted order; ds_down reads the published grouping.
-constexpr int kDsGivenRoutes = 2;
-bool decode_stream_fits(int T, int K, int E, int H, int I);
-void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,
-                      int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,
-                      const Grouping& g, uint32_t* status, uint16_t* h, hipStream_t s);
-void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,
-                    const Grouping& g, float* P, hipStream_t s);
-
 // Few tokens (decode_small): the down GEMV fused with the combine
-// (y[t] = bf16(fma(rm, sum_k gate * out, residual)), rounded as the
+// (y[t] = st(fma(rm, sum_k gate * out, residual)), rounded as the
 // separate down GEMV and combine round it).
-bool decode_small(int T, int K);
-void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,
-                            const int32_t* inverse, int T, int K, int E, int H, int I, const tfm_affine& down,
-                            const uint16_t* residual, float rmul, uint16_t* y, hipStream_t s);
+// One set per storage dtype: ds_bf16 (dstream.hip), ds_f16 (dstream_f16.hip).
+constexpr int kDsGivenRoutes = 2;
+#define TFM_DS_DECLS                                                                                     \
+  bool decode_stream_fits(int T, int K, int E, int H, int I);                                             \
+  void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,  \
+                        int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,  \
+                        const Grouping& g, uint32_t* status, uint16_t* h, hipStream_t s);                 \
+  void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,      \
+                      const Grouping& g, float* P, hipStream_t s);                                        \
+  bool decode_small(int T, int K);                                                                        \
+  void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,            \
+                              const int32_t* inverse, int T, int K, int E, int H, int I,                  \
+                              const tfm_affine& down, const uint16_t* residual, float rmul, uint16_t* y, \
+                              hipStream_t s);
+namespace ds_bf16 { TFM_DS_DECLS }
+namespace ds_f16 { TFM_DS_DECLS }
+#undef TFM_DS_DECLS
+inline bool decode_stream_fits(int T, int K, int E, int H, int I) { return ds_bf16::decode_stream_fits(T, K, E, H, I); }
+inline bool decode_small(int T, int K) { return ds_bf16::decode_small(T, K); }
+inline void launch_ds_gateup(bool f16, int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx,
+                             float* gates, int T, int K, int E, int H, int I, const tfm_affine& gate,
+                             const tfm_affine& up, const Grouping& g, uint32_t* status, uint16_t* h,
+                             hipStream_t s) {
+  if (f16)
+    ds_f16::launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s);
+  else
+    ds_bf16::launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s);
+}
+inline void launch_ds_down(bool f16, const uint16_t* hsorted, int H, int I, int max_active,
+                           const tfm_affine& down, const Grouping& g, float* P, hipStream_t s) {
+  if (f16)
+    ds_f16::launch_ds_down(hsorted, H, I, max_active, down, g, P, s);
+  else
+    ds_bf16::launch_ds_down(hsorted, H, I, max_active, down, g, P, s);
+}
+inline void launch_ds_down_combine(bool f16, const uint16_t* hsorted, const int32_t* idx, const float* gates,
+                                   const int32_t* inverse, int T, int K, int E, int H, int I,
+                                   const tfm_affine& down, const uint16_t* residual, float rmul, uint16_t* y,
+                                   hipStream_t s) {
+  if (f16)
+    ds_f16::launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s);
+  else
+    ds_bf16::launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s);
+}
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
 void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
@@ -185,7 +217,7 @@ void launch_ggemm_plain(const uint16_t* x, RowMap rm, const Grouping& g, int64_t
 // Combine of gate-weighted fp32 rows (decode path):
 //   y[t, c] = bf16(residual[t, c] + rm * sum_k P[inverse[t*K+k], c])   (k ascending)
 // Routes whose sorted position is >= *n_valid (bad expert ids) contribute 0.
-void launch_combine_sorted(const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
+void launch_combine_sorted(bool f16, const float* P, const int32_t* inverse, const int32_t* n_valid, int T,
                            int K, int H, const uint16_t* residual, float rmul, uint16_t* y,
                            hipStream_t s);
 // Combine of bf16 expert-output rows (prefill path):
