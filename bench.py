@@ -227,7 +227,7 @@ def dominant_roofline(r: Runner, stages):
     U = r.distinct_experts()
     H, I = g.hidden, g.intermediate
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
-    streaming = r.wl.bits == 4 and r.wl.dtype == "bf16" and r.wl.router == "dense"
+    streaming = r.wl.bits == 4  # the streaming decode kernels (bf16 or f16 storage)
     if r.wl.name in DECODE:
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)

@@ -46,8 +46,7 @@ extern "C" {
 /* ---- enums ----------------------------------------------------------- */
 #define TFM_DTYPE_BF16 0 /* activations, scales and biases in bf16         */
 #define TFM_DTYPE_F16 1  /* IEEE half: TriFuse's shipped packs; needs the
-                            affine router, runs the grouped GEMM at every
-                            batch size                                    */
+                            affine router                                 */
 
 #define TFM_ROUTE_OLMOE 0   /* softmax over E, top-K probabilities         */
 #define TFM_ROUTE_GRANITE 1 /* top-K logits, softmax over the K selected   */
