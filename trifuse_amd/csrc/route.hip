@@ -290,8 +290,7 @@ template <bool F16, int BITS>
 __global__ __launch_bounds__(256) void dequant_router_kernel(const uint32_t* __restrict__ q,
                                                              const uint16_t* __restrict__ sc,
                                                              const uint16_t* __restrict__ bi,
-                                                             int64_t words, int H,
-                                                             uint16_t* __restrict__ w) {
+                                                             int64_t words, uint16_t* __restrict__ w) {
   constexpr int PER = 32 / BITS;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -317,7 +316,6 @@ __global__ __launch_bounds__(256) void dequant_router_kernel(const uint32_t* __r
     v.y = out[2] | ((uint32_t)out[3] << 16);
     *reinterpret_cast<uint2*>(w + k0) = v;
   }
-  (void)H;
 }
 
 void launch_dequant_router(bool f16, int bits, const tfm_affine& r, int E, int H, uint16_t* w,
@@ -329,13 +327,13 @@ void launch_dequant_router(bool f16, int bits, const tfm_affine& r, int E, int H
   const uint16_t* sc = static_cast<const uint16_t*>(r.scales);
   const uint16_t* bi = static_cast<const uint16_t*>(r.biases);
   if (f16 && bits == 8)
-    dequant_router_kernel<true, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
+    dequant_router_kernel<true, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, w);
   else if (f16)
-    dequant_router_kernel<true, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
+    dequant_router_kernel<true, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, w);
   else if (bits == 8)
-    dequant_router_kernel<false, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
+    dequant_router_kernel<false, 8><<<blocks, 256, 0, s>>>(q, sc, bi, words, w);
   else
-    dequant_router_kernel<false, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, H, w);
+    dequant_router_kernel<false, 4><<<blocks, 256, 0, s>>>(q, sc, bi, words, w);
   check_hip(hipGetLastError(), "router dequant launch");
 }
 

@@ -409,6 +409,8 @@ class MoEBlock:
             mw.router_affine = _affine(w.router_q, w.router_s, w.router_b)
             mw.router_bits = rb
         elif router:
+            if w.router is None:
+                raise ValueError("a dense-router block needs weights.router [E, H]")
             _dev(w.router, "router")
             _check_dtype(w.router, self.dtype, "router")
             if tuple(w.router.shape) != (E, H):
