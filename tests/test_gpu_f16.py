@@ -162,3 +162,27 @@ def test_f16_decode_paths_agree(gpu):
     assert torch.equal(y8, y8h)
     assert torch.equal(y2, y3[:2]) and torch.equal(y1, y3[:1])
     assert torch.equal(y3, y8[:3])
+
+
+@pytest.mark.parametrize("T", [4, 300])
+def test_f16_expert_routes_callable(gpu, T):
+    # NativeMoEExpertHook::GPUCallable with half storage: expert-sorted rows
+    # whose gate-weighted sum per token is the block's output.
+    geom = wl.OLMOE
+    log(f"f16 expert_routes T={T}")
+    gpu_dev = torch.device("cuda:0")
+    layer = wl.make_layer(geom, 4, gpu_dev, seed_tag="f16routes", dtype=F16, affine_router=True)
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    blk = _block(geom)
+    x = wl.make_x(geom, T, tag="f16routes_x", dtype=F16).to(gpu_dev)
+    y, idx, gates = blk.forward(x, wts, return_routes=True)
+    N = T * geom.top_k
+    tok = torch.arange(N, device=gpu_dev, dtype=torch.int32) // geom.top_k
+    out, inv = blk.expert_routes(x, tok, idx.reshape(-1), False, wts)
+    torch.cuda.synchronize()
+    assert out.dtype == F16
+    order = np.argsort(idx.cpu().numpy().reshape(-1), kind="stable")
+    np.testing.assert_array_equal(inv.cpu().numpy(), np.argsort(order))
+    rows = oracle.st_to_f32(u16(out), "f16")[inv.cpu().numpy()]
+    comb = (rows * gates.cpu().numpy().reshape(-1)[:, None]).reshape(T, geom.top_k, -1).sum(1)
+    assert max_rel(comb, oracle.st_to_f32(u16(y), "f16")) <= BLOCK_TOL
