@@ -110,3 +110,36 @@ def test_block_8bit_rejects_4bit_weights(gpu):
     x = wl.make_x(geom, 2, tag="eightbit_mismatch").to(gpu)
     with pytest.raises(ValueError, match="shape"):
         _block8(geom).forward(x, tmoe.ExpertWeights.from_layer(layer))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_8bit_decode_paths_agree(gpu, dtype):
+    # At decode shapes 8-bit blocks take the streaming kernels (each byte code
+    # dotted as its two nibbles): against the oracle at eight tokens, the hook
+    # equal to the whole block, and one or two tokens equal to the same tokens
+    # of a three-token batch.
+    geom = wl.OLMOE
+    dt = "f16" if dtype == torch.float16 else "bf16"
+    log(f"8-bit decode agreement {dt}")
+    layer = wl.make_layer(geom, 2, gpu, seed_tag="eightdec", bits=8, dtype=dtype,
+                          affine_router=dtype == torch.float16)
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    blk = tmoe.MoEBlock(geom.hidden, geom.intermediate, geom.experts, geom.top_k, route=geom.route,
+                        residual_multiplier=0.5, bits=8, dtype=dtype,
+                        router="affine" if dtype == torch.float16 else "dense")
+    x = wl.make_x(geom, 8, tag="eightdec_x", dtype=dtype).to(gpu)
+    res = wl.make_x(geom, 8, tag="eightdec_r", dtype=dtype).to(gpu)
+    y8, idx, gates = blk.forward(x, wts, residual=res, return_routes=True)
+    y8h = blk.experts(x, idx, gates, wts, residual=res)
+    y3 = blk.forward(x[:3].contiguous(), wts, residual=res[:3].contiguous())
+    y2 = blk.forward(x[:2].contiguous(), wts, residual=res[:2].contiguous())
+    y1 = blk.forward(x[:1].contiguous(), wts, residual=res[:1].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(y8, y8h)
+    assert torch.equal(y2, y3[:2]) and torch.equal(y1, y3[:1]) and torch.equal(y3, y8[:3])
+    lay = np_layer(layer)
+    ref = oracle.moe_reference(u16(x), idx.cpu().numpy(), gates.cpu().numpy(), lay, residual=u16(res),
+                               rm=0.5, dtype=dt)
+    err = max_rel(oracle.st_to_f32(u16(y8), dt), ref)
+    log(f"  max_rel {err:.2e}")
+    assert err <= BLOCK_TOL

@@ -20,7 +20,8 @@ LIBDIR = PKG / "lib"
 OBJDIR = LIBDIR / "obj"
 LIBNAME = "libtrifuse_moe.so"
 SOURCES = ["capi.hip", "route.hip", "group.hip", "gemv.hip", "decode.hip", "ggemm.hip", "combine.hip",
-           "norm.hip", "dstream.hip", "dstream_f16.hip"]
+           "norm.hip", "dstream.hip", "dstream_f16.hip", "dstream_i8.hip",
+           "dstream_f16_i8.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 from float code.

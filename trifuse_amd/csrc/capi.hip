@@ -155,11 +155,10 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // The decode path (routing per token, grouping in the gate/up prologue)
 // applies when every route fits one grouping thread and both matmul widths
 // fit one 32-element chunk per lane.
-// The streaming decode kernels read 4-bit weights (bf16 or half storage; an
-// affine router is dequantised first). 8-bit blocks route like prefill and
-// run the grouped GEMM at every batch size.
+// The streaming decode kernels read 4-bit or 8-bit weights in bf16 or half
+// storage (an affine router is dequantised first).
 static bool fused_decode(const tfm_geometry& g, int64_t R) {
-  return g.bits == 4 && R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
+  return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
 
 struct GroupWs {
@@ -231,8 +230,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const int64_t R = T * K;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
   const bool small = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
-  // The standalone GEMV kernels (gemv.hip) are bf16 only.
-  const bool gemv = small && !f16;
+  // The standalone GEMV kernels (gemv.hip) are 4-bit bf16 only.
+  const bool gemv = small && !f16 && g.bits == 4;
   if (!grouped && small && decode_stream_fits((int)T, K, E, H, I)) {
     // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
     // shapes, so both entry points give bit-identical results.
@@ -241,19 +240,19 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     gd.gates_sorted = ws.gates_sorted;
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ds_gateup(f16, kDsGivenRoutes, x, nullptr, const_cast<int32_t*>(idx), const_cast<float*>(gates),
+      launch_ds_gateup(f16, g.bits, kDsGivenRoutes, x, nullptr, const_cast<int32_t*>(idx), const_cast<float*>(gates),
                        (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s);
     }
     if (decode_small((int)T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, ws.h, idx, gates, ws.grp.inverse, (int)T, K, E, H, I, w->down, residual,
+      launch_ds_down_combine(f16, g.bits, ws.h, idx, gates, ws.grp.inverse, (int)T, K, E, H, I, w->down, residual,
                              g.residual_multiplier, y, s);
       return;
     }
     const int max_active = (int)(R < E ? R : E);
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down(f16, ws.h, H, I, max_active, w->down, gd, ws.P, s);
+      launch_ds_down(f16, g.bits, ws.h, H, I, max_active, w->down, gd, ws.P, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
     launch_combine_sorted(f16, ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
@@ -332,7 +331,7 @@ int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
     tfm_plan* p = new tfm_plan{};
     p->g = *geometry;
     p->device = dev;
-    p->gemv_max_routes = geometry->bits == 4 ? gemv_threshold() : -1;
+    p->gemv_max_routes = gemv_threshold();
     *plan_out = p;
   });
 }
@@ -572,19 +571,19 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
     {
       // Top-k and grouping run in this kernel's prologue.
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_ds_gateup(f16, g.route, static_cast<const uint16_t*>(x), ws.logits, ws.idx, ws.gates, T, K, E, H,
+      launch_ds_gateup(f16, g.bits, g.route, static_cast<const uint16_t*>(x), ws.logits, ws.idx, ws.gates, T, K, E, H,
                        I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s);
     }
     const int max_active = (int)(R < E ? R : E);
     if (decode_small(T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, ws.h, ws.idx, ws.gates, ws.grp.inverse, T, K, E, H, I, weights->down,
+      launch_ds_down_combine(f16, g.bits, ws.h, ws.idx, ws.gates, ws.grp.inverse, T, K, E, H, I, weights->down,
                              static_cast<const uint16_t*>(residual), g.residual_multiplier,
                              static_cast<uint16_t*>(y), s);
     } else {
       {
         StageScope st(TFM_STAGE_DOWN, s);
-        launch_ds_down(f16, ws.h, H, I, max_active, weights->down, gd, ws.P, s);
+        launch_ds_down(f16, g.bits, ws.h, H, I, max_active, weights->down, gd, ws.P, s);
       }
       StageScope st(TFM_STAGE_COMBINE, s);
       launch_combine_sorted(f16, ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
@@ -596,7 +595,7 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
                                    reinterpret_cast<int32_t*>(gates_out), R, s);
     return;
   }
-  if (fused_decode(g, R) && !f16 && g.router == TFM_ROUTER_DENSE) {
+  if (fused_decode(g, R) && !f16 && g.bits == 4 && g.router == TFM_ROUTER_DENSE) {
     {
       StageScope st(TFM_STAGE_ROUTER, s);
       launch_decode_route(g.route, static_cast<const uint16_t*>(x),
@@ -762,7 +761,8 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     const RowMap rm{grp.order, token_indices, 1, tokens, &hdr->status};
     const int max_active = (int)(n_routes < E ? n_routes : E);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
-    if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048 && g.dtype == TFM_DTYPE_BF16) {
+    if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048 && g.dtype == TFM_DTYPE_BF16 &&
+        g.bits == 4) {
       launch_gemv_gateup(xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
       launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
       launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);

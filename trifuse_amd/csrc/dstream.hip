@@ -39,8 +39,15 @@
 #ifndef TFM_DS_F16
 #define TFM_DS_F16 0
 #endif
-#if TFM_DS_F16
+#ifndef TFM_DS_BITS
+#define TFM_DS_BITS 4
+#endif
+#if TFM_DS_F16 && TFM_DS_BITS == 8
+#define TFM_DS_NS ds_f16_i8
+#elif TFM_DS_F16
 #define TFM_DS_NS ds_f16
+#elif TFM_DS_BITS == 8
+#define TFM_DS_NS ds_bf16_i8
 #else
 #define TFM_DS_NS ds_bf16
 #endif
@@ -49,6 +56,14 @@ namespace tfm {
 namespace TFM_DS_NS {
 
 constexpr bool kF16 = TFM_DS_F16 != 0;
+// Code width. A 32-element chunk is 16 bytes of nibbles (4-bit) or 32 bytes
+// of byte codes (8-bit). An 8-bit code c = lo + 16 hi is dotted as its two
+// nibbles with the same (base + nibble) trick: sum x (base+lo) + 16 sum x
+// (base+hi) = sum x c + 17 base sum x.
+constexpr int kBits = TFM_DS_BITS;
+static_assert(kBits == 4 || kBits == 8, "4-bit or 8-bit codes");
+constexpr int kQW = kBits / 4;  // 16-byte loads per 32-element chunk
+__host__ __device__ constexpr float code_corr() { return (kBits == 4 ? 1.0f : 17.0f) * code_base(kF16); }
 
 constexpr int kDsCostUnpack = 2;  // item cost = kDsCostUnpack + routes of its expert
 constexpr int kDsSmallT = 2;      // tokens up to which the three-kernel layer is used
@@ -249,7 +264,7 @@ __device__ __forceinline__ void ds_rank_group(DsGroupLds& L, const uint16_t* __r
 // Raw loads of one chunk of one row: 16 packed bytes and its group's scale and
 // bias (bf16 in the low half).
 struct DsRaw {
-  uint4 q;
+  uint4 q[kQW];
   uint32_t s, b;
 };
 
@@ -259,7 +274,7 @@ struct DsMat {
 
 // Buffer resources over expert e's rows of one matrix; rows >= N read zero.
 __device__ __forceinline__ DsMat ds_mat(const tfm_affine& m, int e, int N, int kin) {
-  const uint32_t qrow = (uint32_t)kin / 2, srow = (uint32_t)kin / 32;
+  const uint32_t qrow = (uint32_t)kin * kBits / 8, srow = (uint32_t)kin / 32;
   DsMat d;
   d.q = make_rsrc(reinterpret_cast<const char*>(m.q) + (size_t)e * N * qrow, (uint32_t)N * qrow);
   d.s = make_rsrc(static_cast<const char*>(m.scales) + (size_t)e * N * srow, (uint32_t)N * srow);
@@ -270,13 +285,15 @@ __device__ __forceinline__ DsMat ds_mat(const tfm_affine& m, int e, int N, int k
 // Chunk c (c < C) of row n for lane column ll: element offset 32 * (16c + ll).
 template <int C>
 __device__ __forceinline__ void ds_load_row(const DsMat& m, int n, int kin, int ll, DsRaw (&w)[C]) {
-  const uint32_t qrow = (uint32_t)kin / 2, srow = (uint32_t)kin / 32;
+  const uint32_t qrow = (uint32_t)kin * kBits / 8, srow = (uint32_t)kin / 32;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const uint32_t k = 16u * c + ll;
-    const uint32_t qo = (uint32_t)n * qrow + 16u * k;
+    const uint32_t qo = (uint32_t)n * qrow + 16u * kQW * k;
     const uint32_t so = (uint32_t)n * srow + 2u * (k >> 1);
-    w[c].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.q, qo, 0, 0));
+#pragma unroll
+    for (int j = 0; j < kQW; ++j)
+      w[c].q[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.q, qo + 16u * j, 0, 0));
     w[c].s = __builtin_amdgcn_raw_buffer_load_b16(m.s, so, 0, 0);
     w[c].b = __builtin_amdgcn_raw_buffer_load_b16(m.b, so, 0, 0);
   }
@@ -333,6 +350,48 @@ struct DsGateUpArgs {
   uint16_t* h;  // [R, I]
 };
 
+// Codes of x group q of a chunk (elements 8q..8q+7, staged as the pairs
+// (0,2) (4,6) (1,3) (5,7) in v) dotted with v: d += sum x (base + code)
+// (4-bit); d += sum x (base + lo), dh += sum x (base + hi) (8-bit).
+__device__ __forceinline__ void ds_word_dot(const DsRaw& r, int q, const uint4& v, float& d, float& dh) {
+  if constexpr (kBits == 4) {
+    // Opaque copy: keeps the unpack inside the route loop (hoisted out of
+    // it, the unpacked item would need many more registers).
+    uint32_t wq = word_of(r.q[0], q);
+    asm volatile("" : "+v"(wq));
+    uint32_t p[4];
+    unpack_word_st<kF16>(wq, p);
+    d = dot2_st<kF16>(p[0], v.x, d);
+    d = dot2_st<kF16>(p[1], v.y, d);
+    d = dot2_st<kF16>(p[2], v.z, d);
+    d = dot2_st<kF16>(p[3], v.w, d);
+    (void)dh;
+  } else {
+    // Words 2q and 2q+1 of the chunk hold codes 8q..8q+3 and 8q+4..8q+7.
+    uint32_t wa = word_of(r.q[q >> 1], (2 * q) & 3), wb = word_of(r.q[q >> 1], (2 * q + 1) & 3);
+    asm volatile("" : "+v"(wa), "+v"(wb));
+    const uint32_t magic = kF16 ? 0x64646464u : 0x43434343u;
+    const uint32_t la = wa & 0x0f0f0f0fu, ha = (wa >> 4) & 0x0f0f0f0fu;
+    const uint32_t lb = wb & 0x0f0f0f0fu, hb = (wb >> 4) & 0x0f0f0f0fu;
+    d = dot2_st<kF16>(__builtin_amdgcn_perm(magic, la, 0x04020400u), v.x, d);   // codes 0, 2
+    d = dot2_st<kF16>(__builtin_amdgcn_perm(magic, lb, 0x04020400u), v.y, d);   // codes 4, 6
+    d = dot2_st<kF16>(__builtin_amdgcn_perm(magic, la, 0x04030401u), v.z, d);   // codes 1, 3
+    d = dot2_st<kF16>(__builtin_amdgcn_perm(magic, lb, 0x04030401u), v.w, d);   // codes 5, 7
+    dh = dot2_st<kF16>(__builtin_amdgcn_perm(magic, ha, 0x04020400u), v.x, dh);
+    dh = dot2_st<kF16>(__builtin_amdgcn_perm(magic, hb, 0x04020400u), v.y, dh);
+    dh = dot2_st<kF16>(__builtin_amdgcn_perm(magic, ha, 0x04030401u), v.z, dh);
+    dh = dot2_st<kF16>(__builtin_amdgcn_perm(magic, hb, 0x04030401u), v.w, dh);
+  }
+}
+
+// s * sum x w over one chunk from its code dots: fma(s, d [+ 16 dh], c * sum x).
+__device__ __forceinline__ float ds_chunk_value(float s, float d, float dh, float cxs) {
+  if constexpr (kBits == 4)
+    return __builtin_fmaf(s, d, cxs);
+  else
+    return __builtin_fmaf(s, __builtin_fmaf(16.0f, dh, d), cxs);
+}
+
 template <int C>
 struct DsGU {
   DsRaw g[C], u[C];
@@ -355,29 +414,16 @@ __device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restr
     for (int q = 0; q < 4; ++q) v[q] = xs[(tok * 4 + q) * nch + k];
     const float xsm = xsum[tok * nch + k];
     const float sg = st2f<kF16>((uint16_t)w.g[c].s), su = st2f<kF16>((uint16_t)w.u[c].s);
-    const float cg = __builtin_fmaf(-code_base(kF16), sg, st2f<kF16>((uint16_t)w.g[c].b));
-    const float cu = __builtin_fmaf(-code_base(kF16), su, st2f<kF16>((uint16_t)w.u[c].b));
-    float dg = 0.0f, du = 0.0f;
+    const float cg = __builtin_fmaf(-code_corr(), sg, st2f<kF16>((uint16_t)w.g[c].b));
+    const float cu = __builtin_fmaf(-code_corr(), su, st2f<kF16>((uint16_t)w.u[c].b));
+    float dg = 0.0f, du = 0.0f, dgh = 0.0f, duh = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      // Opaque copies keep the unpack inside the route loop: hoisted out of
-      // it, the unpacked item would need 128 more registers.
-      uint32_t wg = word_of(w.g[c].q, q), wu = word_of(w.u[c].q, q);
-      asm volatile("" : "+v"(wg), "+v"(wu));
-      uint32_t pg[4], pu[4];
-      unpack_word_st<kF16>(wg, pg);
-      unpack_word_st<kF16>(wu, pu);
-      dg = dot2_st<kF16>(pg[0], v[q].x, dg);
-      du = dot2_st<kF16>(pu[0], v[q].x, du);
-      dg = dot2_st<kF16>(pg[1], v[q].y, dg);
-      du = dot2_st<kF16>(pu[1], v[q].y, du);
-      dg = dot2_st<kF16>(pg[2], v[q].z, dg);
-      du = dot2_st<kF16>(pu[2], v[q].z, du);
-      dg = dot2_st<kF16>(pg[3], v[q].w, dg);
-      du = dot2_st<kF16>(pu[3], v[q].w, du);
+      ds_word_dot(w.g[c], q, v[q], dg, dgh);
+      ds_word_dot(w.u[c], q, v[q], du, duh);
     }
-    ag += __builtin_fmaf(sg, dg, cg * xsm);
-    au += __builtin_fmaf(su, du, cu * xsm);
+    ag += ds_chunk_value(sg, dg, dgh, cg * xsm);
+    au += ds_chunk_value(su, du, duh, cu * xsm);
   }
 }
 
@@ -518,27 +564,18 @@ __device__ __forceinline__ void ds_dn_dot(const DsDn<C, RG>& w, const uint4* __r
 #pragma unroll
     for (int q = 0; q < 4; ++q) v[q] = xs[(t * 4 + q) * nch + k];
     const float xsm = xsum[t * nch + k];
-    float d[RG];
+    float d[RG], dh[RG];
 #pragma unroll
-    for (int g = 0; g < RG; ++g) d[g] = 0.0f;
+    for (int g = 0; g < RG; ++g) d[g] = dh[g] = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int g = 0; g < RG; ++g) {
-        uint32_t wq = word_of(w.r[g][c].q, q);
-        asm volatile("" : "+v"(wq));  // keeps the unpack inside the route loop
-        uint32_t p[4];
-        unpack_word_st<kF16>(wq, p);
-        d[g] = dot2_st<kF16>(p[0], v[q].x, d[g]);
-        d[g] = dot2_st<kF16>(p[1], v[q].y, d[g]);
-        d[g] = dot2_st<kF16>(p[2], v[q].z, d[g]);
-        d[g] = dot2_st<kF16>(p[3], v[q].w, d[g]);
-      }
+      for (int g = 0; g < RG; ++g) ds_word_dot(w.r[g][c], q, v[q], d[g], dh[g]);
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
       const float sc = st2f<kF16>((uint16_t)w.r[g][c].s);
-      const float cc = __builtin_fmaf(-code_base(kF16), sc, st2f<kF16>((uint16_t)w.r[g][c].b));
-      acc[g] += __builtin_fmaf(sc, d[g], cc * xsm);
+      const float cc = __builtin_fmaf(-code_corr(), sc, st2f<kF16>((uint16_t)w.r[g][c].b));
+      acc[g] += ds_chunk_value(sc, d[g], dh[g], cc * xsm);
     }
   }
 }

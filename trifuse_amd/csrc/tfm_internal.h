@@ -115,7 +115,8 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
 // Few tokens (decode_small): the down GEMV fused with the combine
 // (y[t] = st(fma(rm, sum_k gate * out, residual)), rounded as the
 // separate down GEMV and combine round it).
-// One set per storage dtype: ds_bf16 (dstream.hip), ds_f16 (dstream_f16.hip).
+// One set per storage dtype and code width: ds_bf16 (dstream.hip), ds_f16
+// (dstream_f16.hip), ds_bf16_i8 (dstream_i8.hip), ds_f16_i8 (dstream_f16_i8.hip).
 constexpr int kDsGivenRoutes = 2;
 #define TFM_DS_DECLS                                                                                     \
   bool decode_stream_fits(int T, int K, int E, int H, int I);                                             \
@@ -131,34 +132,41 @@ constexpr int kDsGivenRoutes = 2;
                               hipStream_t s);
 namespace ds_bf16 { TFM_DS_DECLS }
 namespace ds_f16 { TFM_DS_DECLS }
+namespace ds_bf16_i8 { TFM_DS_DECLS }
+namespace ds_f16_i8 { TFM_DS_DECLS }
 #undef TFM_DS_DECLS
 inline bool decode_stream_fits(int T, int K, int E, int H, int I) { return ds_bf16::decode_stream_fits(T, K, E, H, I); }
 inline bool decode_small(int T, int K) { return ds_bf16::decode_small(T, K); }
-inline void launch_ds_gateup(bool f16, int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx,
-                             float* gates, int T, int K, int E, int H, int I, const tfm_affine& gate,
-                             const tfm_affine& up, const Grouping& g, uint32_t* status, uint16_t* h,
-                             hipStream_t s) {
-  if (f16)
-    ds_f16::launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s);
-  else
-    ds_bf16::launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s);
+// The build for storage dtype (f16: IEEE half, else bf16) and code width bits.
+#define TFM_DS_PICK(f16, bits, call)      \
+  do {                                    \
+    if ((bits) == 8 && (f16))             \
+      ds_f16_i8::call;                    \
+    else if ((bits) == 8)                 \
+      ds_bf16_i8::call;                   \
+    else if (f16)                         \
+      ds_f16::call;                       \
+    else                                  \
+      ds_bf16::call;                      \
+  } while (0)
+inline void launch_ds_gateup(bool f16, int bits, int mode, const uint16_t* x, const uint16_t* logits,
+                             int32_t* idx, float* gates, int T, int K, int E, int H, int I,
+                             const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
+                             uint32_t* status, uint16_t* h, hipStream_t s) {
+  TFM_DS_PICK(f16, bits, launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s));
 }
-inline void launch_ds_down(bool f16, const uint16_t* hsorted, int H, int I, int max_active,
+inline void launch_ds_down(bool f16, int bits, const uint16_t* hsorted, int H, int I, int max_active,
                            const tfm_affine& down, const Grouping& g, float* P, hipStream_t s) {
-  if (f16)
-    ds_f16::launch_ds_down(hsorted, H, I, max_active, down, g, P, s);
-  else
-    ds_bf16::launch_ds_down(hsorted, H, I, max_active, down, g, P, s);
+  TFM_DS_PICK(f16, bits, launch_ds_down(hsorted, H, I, max_active, down, g, P, s));
 }
-inline void launch_ds_down_combine(bool f16, const uint16_t* hsorted, const int32_t* idx, const float* gates,
-                                   const int32_t* inverse, int T, int K, int E, int H, int I,
-                                   const tfm_affine& down, const uint16_t* residual, float rmul, uint16_t* y,
-                                   hipStream_t s) {
-  if (f16)
-    ds_f16::launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s);
-  else
-    ds_bf16::launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s);
+inline void launch_ds_down_combine(bool f16, int bits, const uint16_t* hsorted, const int32_t* idx,
+                                   const float* gates, const int32_t* inverse, int T, int K, int E, int H,
+                                   int I, const tfm_affine& down, const uint16_t* residual, float rmul,
+                                   uint16_t* y, hipStream_t s) {
+  TFM_DS_PICK(f16, bits,
+              launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s));
 }
+#undef TFM_DS_PICK
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
 void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
