@@ -183,18 +183,4 @@ void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s)
   check_hip(hipGetLastError(), "copy launch");
 }
 
-__global__ void gates_to_f32_kernel(int from_bf16, const void* __restrict__ src,
-                                    float* __restrict__ dst, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  dst[i] = from_bf16 ? bf2f(static_cast<const uint16_t*>(src)[i]) : static_cast<const float*>(src)[i];
-}
-
-void launch_gates_to_f32(int dtype_native_bf16, const void* src, float* dst, int64_t n,
-                         hipStream_t s) {
-  if (n <= 0) return;
-  gates_to_f32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dtype_native_bf16, src, dst, n);
-  check_hip(hipGetLastError(), "gates launch");
-}
-
 }  // namespace tfm

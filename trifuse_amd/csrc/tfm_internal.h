@@ -237,7 +237,5 @@ void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, co
 // Expert-sorted output rows for the hook (decode path): out[j, c] = bf16(P[j, c])
 void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s);
 void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s);
-void launch_gates_to_f32(int dtype_native_bf16, const void* src, float* dst, int64_t n,
-                         hipStream_t s);
 
 }  // namespace tfm
