@@ -3,30 +3,31 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-extra] [--no-cpu]
 
-A step is one pass of the MoE block over one batch of synthetic input with all
-weights and inputs resident in HBM:
-  olmoe_decode_t8_x16 (default, the headline line): 8 tokens through 16
-  independent OLMoE MoE layers (hidden 2048, 64 experts, top-8, intermediate
-  1024, 4-bit affine g=64 experts, bf16 scales/biases).
-`value` is MoE-layer tok/s = tokens x layers / step time. Every workload
-rotates through 16 distinct layers per step (16 layers exceed the 256 MB
-last-level cache), so per-layer latency is measured with weights from HBM.
+A step is one pass of the MoE block over one batch of synthetic input, with
+all weights and inputs resident in HBM, through 16 distinct, independently
+seeded layers (16 layers exceed the 256 MB last-level cache, so weights
+stream from HBM as they do across a model's layers).
 
-The other workloads (decode 1 token, prefill 512, prefill 4096 with Zipf
-routing, Granite prefill 2048 and decode 32) are measured in the same run and
-reported under "per_workload". Each reports per-layer latency, tok/s, the
-algorithmic bytes (routed experts counted from the step's own routing) and
-FLOPs, and its roofline fraction (HBM for decode, bf16 MFMA for prefill).
+The metric names two configurations, both measured in every default run:
+  olmoe_decode_t1 (the headline, `value`): 1 token through the OLMoE MoE block
+  (hidden 2048, 64 experts, top-8, intermediate 1024, 4-bit affine g=64
+  experts, bf16 scales/biases). `value` = MoE-layer tok/s = tokens x layers /
+  step time; `roofline` is its gate/up kernel against 8 TB/s of HBM.
+  olmoe_prefill_t4096_zipf: 4096 tokens with Zipf(1.1)-skewed routing,
+  reported in `metric_configs` (the last key of the line) with its layer and
+  gate/up kernel against the 2.5 PFLOP/s dense bf16 MFMA peak.
 
-Each workload also reports the step replayed from a HIP graph
-(graph_per_layer_us: the GPU-side time without per-launch host work; the
-replayed output is checked bit for bit against the eager one). `value` is the
-eager (non-graph) rate.
+The other workloads (decode batch 8 over 16 layers, prefill 512, Granite
+prefill 2048 and decode 32, 8-bit and f16 variants) are measured in the same
+run; `workloads` holds their per-layer latency, tok/s and roofline fraction
+(HBM for decode, bf16 MFMA for prefill). Each workload's step is also replayed
+from a HIP graph; the replay is used when its output equals the eager step's
+bit for bit. --report PATH writes the full per-workload record as JSON.
 
-"roofline" is for the dominant kernel of the headline workload, timed with HIP
-events around each of its launches on the stream it runs on. "cpu_baseline"
-is the oracle's MLX-semantics CPU block on the host cores over a bounded
-sample of the same workload.
+"cpu_baseline" is the oracle's MLX-semantics CPU block on the host cores over
+a bounded sample of the headline workload (cycling through its 16 distinct
+layers so the host's last-level cache does not hold the weights), with all
+cores and with one thread.
 """
 from __future__ import annotations
 
@@ -40,7 +41,8 @@ import time
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "MoE-layer tok/s: decode b=1 & prefill 4096; % HBM BW / % MFMA peak"
-HEADLINE = "olmoe_decode_t8_x16"
+HEADLINE = "olmoe_decode_t1"
+PREFILL_METRIC = "olmoe_prefill_t4096_zipf"
 DECODE = {"olmoe_decode_t1", "olmoe_decode_t8_x16", "granite_decode_t32", "olmoe_decode_t8_x16_int8",
           "olmoe_decode_t8_x16_f16"}
 
@@ -57,7 +59,8 @@ def parse():
     p.add_argument("--workload", default=HEADLINE)
     p.add_argument("--no-extra", action="store_true", help="measure the headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=8.0)
+    p.add_argument("--report", default=None, help="write the full per-workload record (JSON) here")
     p.add_argument("--deterministic", action="store_true",
                    help="pass TFM_FLAG_DETERMINISTIC (every path already reduces routes in k order)")
     return p.parse_args()
@@ -264,55 +267,90 @@ def measured_traffic(workload: str):
     return None
 
 
-def cpu_baseline(r: Runner, seconds: float):
-    """The oracle's MLX-semantics CPU block on the host cores over a bounded
-    sample: whole layers of the same workload, cycling through its layers,
-    until `seconds` have elapsed (at least one layer)."""
+def _host_layers(r: Runner, n: int):
+    """Host (numpy) copies of the runner's first n layers for the CPU block."""
     import numpy as np
-
-    import oracle
-
-    model, cores = cpu_info()
-    threads = min(cores, 64)
-    T = r.wl.tokens
-    done_tokens = 0
-    layers = 0
-    elapsed = 0.0
-    used = threads
-    x = r.x.cpu().view(r.torch.int16).numpy().view(np.uint16)
 
     class NpLayer:
         pass
 
-    def host_layer(lay):
+    out = []
+    for lay in r.layers[:n]:
         nl = NpLayer()
         for name in ("gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b", "down_q", "down_s", "down_b"):
             t = getattr(lay, name).cpu()
             setattr(nl, name, t.numpy() if t.dtype == r.torch.int32 else t.view(r.torch.int16).numpy())
         router = lay.router.cpu().view(r.torch.int16).numpy()
         lb = None if lay.logit_bias is None else lay.logit_bias.cpu().numpy()
-        return nl, router, lb
+        out.append((nl, router, lb))
+    return out, r.x.cpu().view(r.torch.int16).numpy().view(np.uint16)
 
-    host = {}
-    nsrc = r.wl.layers
-    while True:
-        li = layers % nsrc
-        if li not in host:
-            host[li] = host_layer(r.layers[li])
-        nl, router, lb = host[li]
+
+def _cpu_rate(r: Runner, host, x, seconds: float, threads: int, min_layers: int):
+    """Whole layers of the CPU block, cycling through `host`, until `seconds`
+    have elapsed and at least `min_layers` layers ran. Returns
+    (tok/s, layers, seconds, threads used)."""
+    import oracle
+
+    T = r.wl.tokens
+    layers, elapsed, used = 0, 0.0, threads
+    while elapsed < seconds or layers < min_layers:
+        nl, router, lb = host[layers % len(host)]
         t0 = time.perf_counter()
         _, _, _, used = oracle.moe_block_cpu(x, nl, r.geom.route, router, lb, top_k=r.geom.top_k,
                                              threads=threads)
         elapsed += time.perf_counter() - t0
-        done_tokens += T
         layers += 1
-        if elapsed >= seconds:
-            break
-    return {"value": done_tokens / elapsed, "unit": "tok/s", "cores": used, "kind": "port",
-            "sample": f"{layers} layer pass(es) x {T} tokens of {r.wl.name} (cycling over its "
-                      f"{min(layers, nsrc)} distinct layer(s)), "
-                      f"{elapsed:.1f} s, {used} OpenMP threads on {model}",
-            "per_layer_ms": elapsed / layers * 1e3}
+    return T * layers / elapsed, layers, elapsed, used
+
+
+def cpu_baseline(r: Runner, seconds: float, one_thread_seconds: float, min_layers: int = 1,
+                 nlayers: int = 16):
+    """The oracle's MLX-semantics CPU block on the host cores over a bounded
+    sample of the same workload: whole layers, cycling through `nlayers`
+    distinct layers (so the host's last-level cache does not serve the
+    weights), with every core and then with one thread."""
+    model, cores = cpu_info()
+    host, x = _host_layers(r, min(nlayers, len(r.layers)))
+    rate, layers, elapsed, used = _cpu_rate(r, host, x, seconds, min(cores, 64), min_layers)
+    out = {"value": rate, "unit": "tok/s", "cores": used, "kind": "port",
+           "sample": f"{layers} layer passes x {r.wl.tokens} tokens of {r.wl.name}, cycling over "
+                     f"{len(host)} distinct layers, {elapsed:.1f} s, {used} OpenMP threads on "
+                     f"{cores} cores of {model}",
+           "per_layer_ms": elapsed / layers * 1e3}
+    if one_thread_seconds > 0:
+        rate1, layers1, elapsed1, _ = _cpu_rate(r, host, x, one_thread_seconds, 1, 1)
+        out["threads_1"] = {"value": rate1, "layers": layers1, "seconds": round(elapsed1, 2),
+                            "per_layer_ms": elapsed1 / layers1 * 1e3}
+    return out
+
+
+def measure(name, dev, args, steps, warmup, deterministic):
+    """Eager, stage and HIP-graph timings of one workload."""
+    r = Runner(name, dev, deterministic)
+    ms, wall = r.time_steps(steps, warmup)
+    st = r.stage_times(max(10, min(steps, 50)))
+    gr = r.graph_time(steps, warmup)
+    rep = workload_report(r, ms, wall, st, gr)
+    rep["roofline_gateup"] = dominant_roofline(r, st)
+    gms, same = gr
+    rep["step_mode"] = "hip_graph" if same else "eager"
+    rep["best_per_layer_us"] = (gms if same else ms) / r.nlayers * 1e3
+    rep["best_tok_per_s"] = r.wl.tokens * r.nlayers / ((gms if same else ms) * 1e-3)
+    return r, rep
+
+
+def compact(name, rep):
+    """Short per-workload summary for the output line."""
+    frac = rep["hbm_frac"] if rep["bound"] == "hbm" else rep["mfma_frac"]
+    frac *= rep["per_layer_us"] / rep["best_per_layer_us"]  # eager -> the reported (best) step time
+    ru = rep["roofline_gateup"]
+    out = {"per_layer_us": round(rep["best_per_layer_us"], 2), "tok_per_s": round(rep["best_tok_per_s"]),
+           "bound": rep["bound"], "layer_frac": round(frac, 4),
+           "gateup_us": round(ru["us_per_launch"], 2), "gateup_frac": round(ru["frac"], 4)}
+    if "down" in rep["stages_us"]:
+        out["down_us"] = round(rep["stages_us"]["down"], 2)
+    return out
 
 
 def main():
@@ -329,59 +367,47 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    from trifuse_amd import workload as wl
 
     log(f"[bench] workload {args.workload}: building resident weights")
-    head = Runner(args.workload, dev, args.deterministic)
-    ms, wall = head.time_steps(args.steps, args.warmup)
-    log(f"[bench] {args.workload}: {ms * 1e3:.1f} us/step")
-    stages = head.stage_times(max(10, min(args.steps, 100)))
-    graph = head.graph_time(args.steps, args.warmup)
-    report = workload_report(head, ms, wall, stages, graph)
-    roof = dominant_roofline(head, stages)
+    head, report = measure(args.workload, dev, args, args.steps, args.warmup, args.deterministic)
+    log(f"[bench] {args.workload}: {report['best_per_layer_us']:.2f} us/layer ({report['step_mode']})")
+    roof = dict(report["roofline_gateup"])
     roof["traffic"] = measured_traffic(args.workload)
 
     per = {args.workload: report}
     if not args.no_extra:
-        from trifuse_amd import workload as wl
-
-        for name, w in wl.WORKLOADS.items():
-            if name == args.workload:
-                continue
+        names = [n for n in wl.WORKLOADS if n != args.workload and n != PREFILL_METRIC]
+        if PREFILL_METRIC != args.workload:
+            names.append(PREFILL_METRIC)  # measured last, printed last
+        for name in names:
             log(f"[bench] workload {name}")
-            r = Runner(name, dev, args.deterministic)
-            steps = args.steps if name in DECODE else max(20, args.steps // 4)
-            m, wa = r.time_steps(steps, max(3, args.warmup // 2))
-            st = r.stage_times(10)
-            gr = r.graph_time(steps, max(3, args.warmup // 2))
-            per[name] = workload_report(r, m, wa, st, gr)
-            per[name]["roofline_gateup"] = dominant_roofline(r, st)
-            if not args.no_cpu and name in ("olmoe_prefill_t4096_zipf", "olmoe_decode_t1"):
-                per[name]["cpu_baseline"] = cpu_baseline(r, 3.0)
+            decode = name in DECODE
+            steps = args.steps if decode else max(10, args.steps // 2)
+            r, rep = measure(name, dev, args, steps, max(3, args.warmup // 2), args.deterministic)
+            per[name] = rep
+            log(f"[bench] {name}: {rep['best_per_layer_us']:.2f} us/layer")
+            if name == PREFILL_METRIC and not args.no_cpu:
+                rep["cpu_baseline"] = cpu_baseline(r, 0.0, 0.0, min_layers=3, nlayers=3)
             del r
             torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
-        cpu = cpu_baseline(head, args.cpu_seconds)
+        cpu = cpu_baseline(head, args.cpu_seconds, max(1.0, args.cpu_seconds / 2))
 
     g = head.geom
-    # The step replayed as one HIP graph (the same kernels on the same resident
-    # inputs, no per-launch host work) is the headline when its output equals
-    # the eager step's bit for bit; the eager figure is reported beside it.
-    gms, gsame = graph
-    head_ms = gms if gsame else ms
     line = {
         "metric": METRIC,
-        "value": head.wl.tokens * head.nlayers / (head_ms * 1e-3),
+        "value": report["best_tok_per_s"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head_ms,
-        "step_mode": "hip_graph" if gsame else "eager",
-        "eager_ms_per_step": ms,
-        "eager_value": report["tok_per_s"],
+        "ms_per_step": report["best_per_layer_us"] * head.nlayers / 1e3,
+        "step_mode": report["step_mode"],
+        "eager_ms_per_step": report["per_layer_us"] * head.nlayers / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -393,8 +419,21 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "per_workload": per,
+        "workloads": {n: compact(n, r) for n, r in per.items()
+                      if n not in (args.workload, PREFILL_METRIC)},
     }
+    mc = {args.workload: compact(args.workload, report)}
+    if PREFILL_METRIC in per:
+        pre = per[PREFILL_METRIC]
+        mc[PREFILL_METRIC] = compact(PREFILL_METRIC, pre)
+        if "cpu_baseline" in pre:
+            mc[PREFILL_METRIC]["cpu_tok_per_s"] = round(pre["cpu_baseline"]["value"], 1)
+    line["metric_configs"] = mc
+    if args.report:
+        with open(args.report, "w") as f:
+            json.dump({"line": line, "per_workload": per}, f, indent=1)
+    for n, c in mc.items():
+        log(f"[bench] {n}: " + json.dumps(c))
     print(json.dumps(line), flush=True)
 
 

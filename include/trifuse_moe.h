@@ -13,6 +13,9 @@
  *    as it is enqueued. Results are valid after the stream is synchronised.
  *  - No call allocates device memory after tfm_plan_create: scratch memory
  *    comes from the caller's workspace (size from the *_workspace_bytes call).
+ *    The first 256 bytes of a workspace hold the device status word: zero
+ *    them once when the workspace is allocated. Kernels only set status bits;
+ *    they stay set across calls until tfm_status_word reads and clears them.
  *  - Every entry point returns an int status (TFM_OK == 0). No C++ exception
  *    crosses the ABI; tfm_last_error() returns the calling thread's message.
  *  - Affine weight layout (identical to MLX / TriFuse packs):
@@ -269,7 +272,9 @@ const char* tfm_stage_name(int32_t stage);
 
 /* ---- diagnostics ----------------------------------------------------- */
 /* Blocking: synchronises `stream`, then reads and clears the device status
- * word kept in `workspace` (TFM_STATUS_* bits). */
+ * word kept in `workspace` (TFM_STATUS_* bits). The bits are sticky: a bad
+ * expert id or row index seen by any call since the last read stays
+ * reported, whatever later calls on the same workspace did. */
 int tfm_status_word(void* workspace, void* stream, uint32_t* status_out);
 
 /* Message of the last failing call on this thread ("" if none). */

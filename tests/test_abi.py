@@ -31,7 +31,7 @@ def test_version_and_stage_names():
     lib = _lib.load()
     assert b"gfx950" in lib.tfm_version()
     assert [lib.tfm_stage_name(i).decode() for i in range(_lib.TFM_STAGE_COUNT)] == \
-        ["router", "topk", "group", "gateup", "down", "combine"]
+        ["router", "topk", "group", "gateup", "down", "combine", "norm"]
     assert lib.tfm_stage_name(99) == b""
 
 
@@ -104,6 +104,14 @@ def test_gather_qmm_argument_checks():
     st = lib.tfm_gather_qmm(None, 4, None, None, 8, ctypes.byref(aff), 4, 128, 256, 64, 4,
                             _lib.TFM_DTYPE_BF16, 0, None, None, 0, None)
     assert st == _lib.TFM_E_INVALID and b"x_row_count" in lib.tfm_last_error()
+    # rows to compute but an empty x: refused before any pointer is read
+    need = lib.tfm_gather_qmm_workspace_bytes(8, 4, 128, 256)
+    buf = ctypes.create_string_buffer(need + 512)
+    base = ctypes.c_void_p((ctypes.addressof(buf) + 255) // 256 * 256)
+    fake = ctypes.c_void_p(16)  # never dereferenced
+    st = lib.tfm_gather_qmm(fake, 0, fake, fake, 8, ctypes.byref(aff), 4, 128, 256, 64, 4,
+                            _lib.TFM_DTYPE_BF16, 0, fake, base, need, None)
+    assert st == _lib.TFM_E_INVALID and b"no rows" in lib.tfm_last_error()
     st = lib.tfm_gather_qmm(None, 8, None, None, 8, ctypes.byref(aff), 4, 96, 256, 64, 4,
                             _lib.TFM_DTYPE_BF16, 0, None, None, 0, None)
     assert st == _lib.TFM_E_UNSUPPORTED and b"multiple of 64" in lib.tfm_last_error()

@@ -34,10 +34,12 @@ def _routes(geom, x_u16, lay, dt):
     return idx, g, logits
 
 
-def _check(geom, T, bits=4, dtype=F16, rm=1.0, tag="f16", layer_id=0):
+def _check(geom, T, bits=4, dtype=F16, rm=1.0, tag="f16", layer_id=0, router_bits=4):
     dt = "f16" if dtype == F16 else "bf16"
     gpu = torch.device("cuda:0")
-    layer = wl.make_layer(geom, layer_id, gpu, seed_tag=tag, bits=bits, dtype=dtype, affine_router=True)
+    layer = wl.make_layer(geom, layer_id, gpu, seed_tag=tag, bits=bits, dtype=dtype, affine_router=True,
+                          router_bits=router_bits)
+    assert layer.router_bits == router_bits
     x = wl.make_x(geom, T, tag=tag + "_x", dtype=dtype)
     res = wl.make_x(geom, T, tag=tag + "_r", dtype=dtype)
     blk = _block(geom, rm=rm, bits=bits, dtype=dtype)
@@ -68,6 +70,14 @@ def test_block_f16_affine_router(gpu, geom_name, T):
 def test_block_f16_8bit(gpu):
     log("moe f16 8-bit T=64")
     _check(wl.OLMOE, 64, bits=8, tag="f16_8bit")
+
+
+@pytest.mark.parametrize("dtype", [F16, torch.bfloat16])
+@pytest.mark.parametrize("T", [1, 8, 300])
+def test_block_8bit_affine_router(gpu, T, dtype):
+    """router_bits = 8: four LSB-first byte codes per router word."""
+    log(f"moe 8-bit affine router {dtype} T={T}")
+    _check(wl.OLMOE, T, dtype=dtype, tag="r8", router_bits=8)
 
 
 @pytest.mark.parametrize("T", [8, 300])

@@ -190,3 +190,64 @@ def test_empty_and_bad_routes(gpu):
     torch.cuda.synchronize()
     assert max_rel(f32(yb), f32(yr)) <= BLOCK_TOL
     assert blk.status_word() == 0
+
+
+def test_status_word_is_sticky(gpu):
+    """A bad expert id stays reported across later good calls until
+    tfm_status_word reads (and clears) the word."""
+    from trifuse_amd import _lib
+
+    geom = wl.OLMOE
+    log("moe status word: bad call, good calls, then read")
+    layer = wl.make_layer(geom, 0, gpu, seed_tag="sticky")
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    blk = _block(geom)
+    for T in (2, 300):  # decode kernels and the prefill grouping
+        x = wl.make_x(geom, T, tag=f"sticky{T}").to(gpu)
+        _, idx, gates = blk.forward(x, wts, return_routes=True)
+        assert blk.status_word() == 0
+        bad = idx.clone()
+        bad[T - 1, 2] = 99
+        blk.experts(x, bad, gates, wts)
+        blk.experts(x, idx, gates, wts)      # good call on the same workspace
+        blk.forward(x, wts)                  # and a good whole-block call
+        torch.cuda.synchronize()
+        assert blk.status_word() & _lib.TFM_STATUS_BAD_EXPERT_ID, f"T={T}: bad id lost"
+        assert blk.status_word() == 0        # read clears
+
+
+def test_host_mirror_rejects_bad_arguments(gpu):
+    """Shape, dtype and device errors raise before any device work."""
+    geom = wl.OLMOE
+    layer = wl.make_layer(geom, 0, gpu, seed_tag="reject")
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    blk = _block(geom)
+    T, K = 4, geom.top_k
+    x = wl.make_x(geom, T, tag="reject").to(gpu)
+    _, idx, gates = blk.forward(x, wts, return_routes=True)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        blk.experts(x, idx.cpu(), gates, wts)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        blk.experts(x, idx, gates.cpu(), wts)
+    with pytest.raises(ValueError, match="gates must be"):
+        blk.experts(x, idx, gates[:, :3].contiguous(), wts)
+    with pytest.raises(ValueError, match="residual"):
+        blk.experts(x, idx, gates, wts, residual=x[:2].contiguous())
+    with pytest.raises(ValueError, match="residual"):
+        blk.experts(x, idx, gates, wts, residual=x.half())
+    with pytest.raises(ValueError, match="router shape"):
+        blk.route(x, layer.router[:, :1024].contiguous())
+    with pytest.raises(ValueError, match="logit_bias"):
+        blk.route(x, layer.router, torch.zeros(geom.experts, device=gpu, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="logit_bias"):
+        blk.route(x, layer.router, torch.zeros(geom.experts - 1, device=gpu))
+    with pytest.raises(ValueError, match="GPU tensor"):
+        blk.expert_routes(x, torch.zeros(8, dtype=torch.int32), idx.reshape(-1)[:8].contiguous(), False, wts)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        blk.expert_routes(x, torch.zeros(8, dtype=torch.int32, device=gpu), idx.reshape(-1)[:8].cpu(), False,
+                          wts)
+    # routes but no tokens: the C ABI refuses before reading x
+    from trifuse_amd._lib import TfmError
+    with pytest.raises(TfmError, match="no tokens"):
+        blk.expert_routes(x[:0], torch.zeros(8, dtype=torch.int32, device=gpu),
+                          idx.reshape(-1)[:8].contiguous(), False, wts)

@@ -34,7 +34,8 @@ TFM_STAGE_GROUP = 2
 TFM_STAGE_GATEUP = 3
 TFM_STAGE_DOWN = 4
 TFM_STAGE_COMBINE = 5
-TFM_STAGE_COUNT = 6
+TFM_STAGE_NORM = 6
+TFM_STAGE_COUNT = 7
 
 _STATUS_NAMES = {
     TFM_E_INVALID: "invalid argument",

@@ -500,6 +500,7 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     GroupWs ws = carve_group(rows, num_experts, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
     if (rows == 0) return;
+    need(x_row_count > 0, "x has no rows to gather from");
     need_ptr(x, "x");
     need_ptr(rhs_indices, "rhs_indices");
     need_ptr(w, "w");
@@ -737,6 +738,7 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     const size_t want = tfm_expert_routes_workspace_bytes(plan, n_routes);
     need_ws(workspace, workspace_bytes, want);
     if (n_routes == 0) return;
+    need(tokens > 0, "routes given but x has no tokens");
     need_ptr(x, "x");
     need_ptr(token_indices, "token_indices");
     need_ptr(expert_ids, "expert_ids");

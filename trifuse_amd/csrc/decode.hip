@@ -36,7 +36,7 @@ struct DecodeGateUpArgs {
   int4* slots;             // [E] per active slot {expert, first route, end route, 0}
   float* gates_sorted;     // [R] gates in sorted order
   uint16_t* h;             // [R, I] SwiGLU output, expert-sorted rows
-  uint32_t* status;        // the call's status word, cleared here
+  uint32_t* status;        // status word (no bits: routes come from the router)
 };
 
 __device__ __forceinline__ uint64_t lanemask_lt64() {
@@ -120,7 +120,6 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
       const int ex = tid < s_act[E] ? s_act[tid] : -1;
       A.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, 0) : make_int4(ex, s_off[ex], s_off[ex + 1], 0);
     }
-    if (tid == 0) *A.status = 0u;
   }
 
   // Gate/up rows: kGemvUnits row units of active expert blockIdx.y.

@@ -256,7 +256,8 @@ __device__ __forceinline__ void ds_rank_group(DsGroupLds& L, const uint16_t* __r
       const int ex = tid < U ? L.act[tid] : -1;
       g.slots[tid] = ex < 0 ? make_int4(-1, 0, 0, U) : make_int4(ex, L.off[ex], L.off[ex + 1], U);
     }
-    if (tid == 0) *status = L.off[E] < R ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
+    // Sticky: bits accumulate until tfm_status_word reads and clears them.
+    if (tid == 0 && L.off[E] < R) atomicOr(status, (uint32_t)TFM_STATUS_BAD_EXPERT_ID);
   }
 }
 

@@ -68,14 +68,13 @@ __global__ __launch_bounds__(64) void superblock_sums_kernel(const int32_t* __re
   if (64 + lane < B) bsum[(int64_t)sb * B + 64 + lane] = s1;
 }
 
-// Grouping of zero routes: offsets all zero, no active expert, status clear.
+// Grouping of zero routes: offsets all zero, no active expert (the status
+// word keeps its bits).
 __global__ void group_empty_kernel(int E, Grouping g, uint32_t* __restrict__ status) {
+  (void)status;
   const int tid = threadIdx.x;
   if (tid <= E) g.offsets[tid] = 0;
-  if (tid == 0) {
-    g.active[E] = 0;
-    *status = 0u;
-  }
+  if (tid == 0) g.active[E] = 0;
 }
 
 static void launch_group_empty(int E, Grouping g, uint32_t* status, hipStream_t s) {
@@ -165,7 +164,8 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
       if (lane < E && t > 0) g.active[__popcll(act & lanemask_lt())] = lane;
       if (lane == 0) {
         g.active[E] = __popcll(act);
-        *status = bad_total > 0 ? (uint32_t)TFM_STATUS_BAD_EXPERT_ID : 0u;
+        // Sticky: bits accumulate until tfm_status_word reads and clears them.
+        if (bad_total > 0) atomicOr(status, (uint32_t)TFM_STATUS_BAD_EXPERT_ID);
       }
     }
   }

@@ -53,6 +53,22 @@ def _dev(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
+def _check_residual(residual: Optional[torch.Tensor], x: torch.Tensor) -> None:
+    if residual is None:
+        return
+    _dev(residual, "residual")
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError("residual geometry/dtype differs")
+
+
+def _check_logit_bias(logit_bias: Optional[torch.Tensor], E: int) -> None:
+    if logit_bias is None:
+        return
+    _dev(logit_bias, "logit_bias")
+    if logit_bias.dtype != torch.float32 or logit_bias.numel() != E:
+        raise ValueError("logit_bias must be fp32 [E]")
+
+
 def _index32(t: torch.Tensor) -> torch.Tensor:
     if t.dtype not in (torch.int32, torch.int64, torch.uint32):
         raise ValueError("indices must be integers")
@@ -88,7 +104,11 @@ def _affine(q, s, b) -> Affine:
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
     # torch's caching allocator returns blocks aligned to at least 512 bytes.
-    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    # The status word lives in the first 256 bytes and is sticky (kernels only
+    # set bits; tfm_status_word clears them), so a fresh workspace starts zeroed.
+    ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    ws[:256].zero_()
+    return ws
 
 
 _DTYPES = {torch.bfloat16: TFM_DTYPE_BF16, torch.float16: TFM_DTYPE_F16}
@@ -124,6 +144,9 @@ def gather_qmm_rows(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, bias
     _dev(x, "x")
     if x.ndim != 2 or x.shape[1] != kin:
         raise ValueError("Native affine expert input differs")
+    _dev(rhs_indices, "rhs_indices")
+    if x_rows is not None:
+        _dev(x_rows, "x_rows")
     rhs = _index32(rhs_indices).reshape(-1)
     rows = rhs.numel()
     xr = None if x_rows is None else _index32(x_rows).reshape(-1)
@@ -416,11 +439,9 @@ class MoEBlock:
             if tuple(w.router.shape) != (E, H):
                 raise ValueError("router shape differs")
             mw.router = w.router.data_ptr()
-            if w.logit_bias is not None:
-                _dev(w.logit_bias, "logit_bias")
-                if w.logit_bias.dtype != torch.float32 or w.logit_bias.numel() != E:
-                    raise ValueError("logit_bias must be fp32 [E]")
-                mw.logit_bias = w.logit_bias.data_ptr()
+        if router and w.logit_bias is not None:
+            _check_logit_bias(w.logit_bias, E)
+            mw.logit_bias = w.logit_bias.data_ptr()
         return mw
 
     # -- entry points --------------------------------------------------------
@@ -429,10 +450,7 @@ class MoEBlock:
         """The whole block: residual + rm * sum_k gate_k * expert_k(x) (y in x's shape).
         With return_routes, also returns (idx [T,K] int32, gates [T,K] fp32)."""
         T = self._check_x(x)
-        if residual is not None:
-            _dev(residual, "residual")
-            if residual.shape != x.shape or residual.dtype != x.dtype:
-                raise ValueError("residual geometry/dtype differs")
+        _check_residual(residual, x)
         mw = self._weights(weights, router=True)
         y = torch.empty_like(x)
         K = self.experts_per_token
@@ -477,12 +495,13 @@ class MoEBlock:
         _dev(router, "router")
         _check_dtype(router, self.dtype, "router")
         K, E = self.experts_per_token, self.num_experts
+        if tuple(router.shape) != (E, self.hidden_size):
+            raise ValueError("router shape differs")
+        _check_logit_bias(logit_bias, E)
         idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
         gdt = self.dtype if self.route_kind == "olmoe" else torch.float32
         gates = torch.empty((T, K), dtype=gdt, device=x.device)
         logits = torch.empty((T, E), dtype=self.dtype, device=x.device)
-        if logit_bias is not None:
-            _dev(logit_bias, "logit_bias")
         ws = self.workspace(T, x.device)
         call("tfm_route", self._plan, x.data_ptr(), T, router.data_ptr(), _ptr(logit_bias),
              logits.data_ptr(), idx.data_ptr(), gates.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
@@ -503,8 +522,7 @@ class MoEBlock:
         gdt = self.dtype if self.route_kind == "olmoe" else torch.float32
         gates = torch.empty((T, K), dtype=gdt, device=x.device)
         logits = torch.empty((T, E), dtype=self.dtype, device=x.device)
-        if logit_bias is not None:
-            _dev(logit_bias, "logit_bias")
+        _check_logit_bias(logit_bias, E)
         aff = _affine(q, scales, biases)
         ws = self.workspace(T, x.device)
         call("tfm_route_affine", self._plan, x.data_ptr(), T, ctypes.byref(aff), bits, _ptr(logit_bias),
@@ -516,12 +534,15 @@ class MoEBlock:
         """NativeMoEExpertHook::execute body (MLXMoEExpertHook.h:43-51) given routes."""
         T = self._check_x(x)
         K = self.experts_per_token
+        _dev(idx, "idx")
+        _dev(gates, "gates")
         idx32 = _index32(idx)
         if idx32.numel() != T * K:
             raise ValueError("indices must be [T, K]")
+        if gates.numel() != T * K:
+            raise ValueError("gates must be [T, K]")
         g32 = gates.to(torch.float32).contiguous()
-        if residual is not None:
-            _dev(residual, "residual")
+        _check_residual(residual, x)
         mw = self._weights(weights, router=False)
         y = torch.empty_like(x)
         ws = self.workspace(T, x.device)
@@ -536,6 +557,8 @@ class MoEBlock:
         """NativeMoEExpertHook::GPUCallable (MLXMoEExpertHook.h:23-30):
         returns (expert-sorted out [N, H], inverse [N]) with out[inverse[i]] for route i."""
         T = self._check_x(x)
+        _dev(token_indices, "token_indices")
+        _dev(expert_ids, "expert_ids")
         tok = _index32(token_indices).reshape(-1)
         eid = _index32(expert_ids).reshape(-1)
         if tok.numel() != eid.numel():

@@ -193,13 +193,14 @@ class LayerWeights:
 
 def make_layer(geom: Geometry, layer: int, device="cpu", zipf: bool = False,
                seed_tag: str = "", bits: int = 4, dtype=torch.bfloat16,
-               affine_router: bool = False) -> LayerWeights:
+               affine_router: bool = False, router_bits: int = 4) -> LayerWeights:
     """Synthetic layer. Codes are uniform over [0, 2^bits) and the bias is
     -2^(bits-1) * scale, so weights are centred on zero; 8-bit scales are
     1/16 of the 4-bit ones, which keeps the weight range the same. Scales,
     biases and the dense router are in `dtype` (bf16 or f16). With
-    affine_router the router is a 4-bit affine matrix (scales U[0.002, 0.006])
-    instead of a dense one."""
+    affine_router the router is an affine matrix of router_bits-bit codes
+    (4-bit scales U[0.002, 0.006], 8-bit scales 1/16 of that, bias
+    -2^(router_bits-1) * scale) instead of a dense one."""
     if bits not in (4, 8):
         raise ValueError("bits must be 4 or 8")
     E, H, I = geom.experts, geom.hidden, geom.intermediate
@@ -217,13 +218,17 @@ def make_layer(geom: Geometry, layer: int, device="cpu", zipf: bool = False,
         w[f"{proj}_s"] = s
         w[f"{proj}_b"] = (s.float() * -float(1 << (bits - 1))).to(dtype)
     if affine_router:
+        if router_bits not in (4, 8):
+            raise ValueError("router_bits must be 4 or 8")
+        rtag = ("router",) if router_bits == 4 else ("router", router_bits)
+        rshrink = 16.0 / (1 << router_bits)
         w["router"] = None
-        w["router_q"] = packed_nibbles((E, H // 8), _key(*tag, "router", "q"), device)
-        rs = uniform_scales((E, H // GROUP), _key(*tag, "router", "s"), device, lo=0.002, hi=0.006,
-                            dtype=dtype)
+        w["router_q"] = packed_nibbles((E, H * router_bits // 32), _key(*tag, *rtag, "q"), device)
+        rs = uniform_scales((E, H // GROUP), _key(*tag, *rtag, "s"), device, lo=0.002 * rshrink,
+                            hi=0.006 * rshrink, dtype=dtype)
         w["router_s"] = rs
-        w["router_b"] = (rs.float() * -8.0).to(dtype)
-        w["router_bits"] = 4
+        w["router_b"] = (rs.float() * -float(1 << (router_bits - 1))).to(dtype)
+        w["router_bits"] = router_bits
     else:
         w["router"] = normal_bf16((E, H), 0.02, _key(*tag, "router"), dtype).to(device)
     lb = zipf_bias(E, _key(*tag, "zipf")).to(device) if zipf else None
