@@ -212,6 +212,23 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens,
                     int32_t* idx_out, float* gates_out, uint32_t flags,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of tfm_moe_forward. No counterpart in the
+ * reference: it is for callers that cannot allocate or pass device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results as tfm_moe_forward, but the
+ * scratch memory is a static device array of TFM_STATIC_SCRATCH_BYTES inside
+ * the library (one per GPU, held until the process ends) instead of a caller
+ * workspace. Calls needing more scratch than that (tfm_workspace_bytes(plan,
+ * tokens) > TFM_STATIC_SCRATCH_BYTES; OLMoE geometry: up to about 700 tokens)
+ * fail with TFM_E_WORKSPACE. The call allocates nothing. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads, other plans) race and must be ordered by the caller. Device
+ * status bits (bad expert ids) of this variant are not reported. */
+#define TFM_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int tfm_moe_forward_static(const tfm_plan* plan, const void* x, int64_t tokens,
+                           const void* residual, const tfm_moe_weights* weights, void* y,
+                           int32_t* idx_out, float* gates_out, uint32_t flags, void* stream);
+
 /* The block with its neighbouring step fused in, as the reference layer runs
  * it (MLXNativeGraniteMoEPrefill.h:485-487):
  *   post = rms_norm(h, norm_weight, eps)          (fast::rms_norm, :485)

@@ -35,6 +35,7 @@ TFM_STAGE_GATEUP = 3
 TFM_STAGE_DOWN = 4
 TFM_STAGE_COMBINE = 5
 TFM_STAGE_NORM = 6
+TFM_STATIC_SCRATCH_BYTES = 64 << 20
 TFM_STAGE_COUNT = 7
 
 _STATUS_NAMES = {
@@ -114,6 +115,8 @@ SIGNATURES = {
     "tfm_moe_forward": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, POINTER(MoeWeights),
                                 c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_size_t,
                                 c_void_p]),
+    "tfm_moe_forward_static": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, POINTER(MoeWeights),
+                                       c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
     "tfm_moe_forward_rmsnorm": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_float,
                                         POINTER(MoeWeights), c_void_p, c_void_p, c_void_p, c_uint32,
                                         c_void_p, c_size_t, c_void_p]),

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -19,6 +20,8 @@ struct tfm_plan {
   tfm_geometry g;
   int device;
   int gemv_max_routes;  // route count up to which the decode GEMV path is used
+  void* scratch;        // device address of this device's static scratch array (or null)
+  std::string scratch_error;  // why `scratch` is null
 };
 
 // Stage profiler: HIP events recorded around each kernel stage of the calls
@@ -32,6 +35,18 @@ struct tfm_profiler {
 };
 
 namespace tfm {
+
+// Workspace of the allocation-free entry point (tfm_moe_forward_static): a
+// file-scope device array. Every GPU the library runs on holds its own copy
+// until the process ends. In host code `scratch` is only a stand-in for the
+// symbol: its device address (per device) comes from hipGetSymbolAddress,
+// taken once per device in tfm_plan_create, and only that address is ever
+// passed to kernels.
+constexpr size_t kStaticScratchBytes = TFM_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxDevices];
 
 static thread_local std::string g_last_error;
 static thread_local tfm_profiler* g_profiler = nullptr;
@@ -296,6 +311,29 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   }
 }
 
+// Device address of the static scratch array on `dev` (the current device),
+// looked up once per device. A failed lookup is recorded in `why` and leaves
+// nullptr: plans still work through the workspace entry points, and
+// tfm_moe_forward_static reports the failure.
+static void* static_scratch(int dev, std::string& why) {
+  if (dev < 0 || dev >= kMaxDevices) {
+    why = "device ordinal beyond the static scratch table";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      why = std::string("hipGetSymbolAddress: ") + hipGetErrorString(err);
+      return nullptr;
+    }
+    g_scratch_addr[dev] = ptr;
+  }
+  return g_scratch_addr[dev];
+}
+
 static void check_weights(const tfm_moe_weights* w, bool router, const tfm_geometry& g) {
   need_ptr(w, "weights");
   if (router && g.router == TFM_ROUTER_DENSE) {
@@ -328,10 +366,14 @@ int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
     check_geometry(*geometry);
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
+    std::string why;
+    void* scr = static_scratch(dev, why);
     tfm_plan* p = new tfm_plan{};
     p->g = *geometry;
     p->device = dev;
     p->gemv_max_routes = gemv_threshold();
+    p->scratch = scr;
+    p->scratch_error = why;
     *plan_out = p;
   });
 }
@@ -677,6 +719,32 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens, const v
     check_weights(weights, true, plan->g);
     BlockWs ws = carve_block(plan->g, tokens, workspace);
     need_ws(workspace, workspace_bytes, ws.bytes);
+    moe_forward_body(plan, x, tokens, residual, weights, y, idx_out, gates_out, flags, ws,
+                     static_cast<hipStream_t>(stream));
+  });
+}
+
+int tfm_moe_forward_static(const tfm_plan* plan, const void* x, int64_t tokens, const void* residual,
+                           const tfm_moe_weights* weights, void* y, int32_t* idx_out, float* gates_out,
+                           uint32_t flags, void* stream) {
+  return guarded([&] {
+    need_ptr(plan, "plan");
+    need(tokens >= 0 && tokens <= INT32_MAX / 64, "tokens out of range");
+    if (tokens == 0) return;
+    need_ptr(x, "x");
+    need_ptr(y, "y");
+    need_align16(x, "x");
+    need_align16(y, "y");
+    if (residual) need_align16(residual, "residual");
+    check_weights(weights, true, plan->g);
+    const size_t want = carve_block(plan->g, tokens, nullptr).bytes;
+    if (want > kStaticScratchBytes)
+      fail(TFM_E_WORKSPACE, "tfm_moe_forward_static: " + std::to_string(tokens) + " tokens need " +
+                                std::to_string(want) + " bytes of scratch, more than the static array's " +
+                                std::to_string(kStaticScratchBytes) + " (use tfm_moe_forward with a workspace)");
+    if (!plan->scratch)
+      fail(TFM_E_HIP, "tfm_moe_forward_static: no static scratch on the plan's device (" + plan->scratch_error + ")");
+    BlockWs ws = carve_block(plan->g, tokens, plan->scratch);
     moe_forward_body(plan, x, tokens, residual, weights, y, idx_out, gates_out, flags, ws,
                      static_cast<hipStream_t>(stream));
   });

@@ -464,6 +464,24 @@ class MoEBlock:
              y.data_ptr(), _ptr(idx), _ptr(gates), flags, ws.data_ptr(), ws.numel(), _stream())
         return (y, idx, gates) if return_routes else y
 
+    def forward_static(self, x: torch.Tensor, weights: ExpertWeights, residual: Optional[torch.Tensor] = None,
+                       return_routes: bool = False):
+        """forward() through the allocation-free entry point (tfm_moe_forward_static):
+        the library's static device scratch instead of a workspace. Calls on
+        one GPU share that scratch and must not overlap."""
+        T = self._check_x(x)
+        _check_residual(residual, x)
+        mw = self._weights(weights, router=True)
+        y = torch.empty_like(x)
+        K = self.experts_per_token
+        idx = gates = None
+        if return_routes:
+            idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+            gates = torch.empty((T, K), dtype=torch.float32, device=x.device)
+        call("tfm_moe_forward_static", self._plan, x.data_ptr(), T, _ptr(residual), ctypes.byref(mw),
+             y.data_ptr(), _ptr(idx), _ptr(gates), 0, _stream())
+        return (y, idx, gates) if return_routes else y
+
     def forward_rmsnorm(self, h: torch.Tensor, weights: ExpertWeights, norm_weight: torch.Tensor,
                         eps: float, return_routes: bool = False):
         """The block with the post-attention RMSNorm fused in, as the reference
