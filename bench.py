@@ -63,7 +63,50 @@ def parse():
     p.add_argument("--report", default=None, help="write the full per-workload record (JSON) here")
     p.add_argument("--deterministic", action="store_true",
                    help="pass TFM_FLAG_DETERMINISTIC (every path already reduces routes in k order)")
+    p.add_argument("--pmc-summary", default=None, metavar="DIR",
+                   help="only summarise the rocprofv3 counter CSVs under DIR (mean per dispatch of "
+                        "every counter, per kernel) as JSON and exit")
+    p.add_argument("--pmc-copy", type=int, default=0, metavar="MIB",
+                   help="only run 5 device-to-device copies of MIB MiB (a kernel of known traffic, to "
+                        "calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return p.parse_args()
+
+
+def pmc_summary(root: str):
+    """Per kernel (name up to its argument list): dispatch count and the mean
+    over its dispatches of every counter in the rocprofv3 --pmc CSV output
+    under `root` (Counter_Value summed over the CSV rows of one dispatch)."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    sums = defaultdict(lambda: defaultdict(float))
+    disp = defaultdict(set)
+    for path in glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                k = row.get("Kernel_Name", "?").split("(")[0]
+                disp[k].add(row.get("Dispatch_Id"))
+                sums[k][row["Counter_Name"]] += float(row["Counter_Value"])
+    out = {k: {"dispatches": len(disp[k]), **{c: v / len(disp[k]) for c, v in sorted(sums[k].items())}}
+           for k in sums}
+    print(json.dumps(out, indent=1), flush=True)
+
+
+def pmc_copy(mib: int, reps: int = 5):
+    """Copies of a known size: under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)
+    each copy dispatch reads and writes exactly `mib` MiB, so counter /
+    (mib * 1024) is the counter's scale in KiB per KiB moved."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copied {mib} MiB x {reps}", flush=True)
 
 
 def cpu_info():
@@ -248,13 +291,14 @@ def dominant_roofline(r: Runner, stages):
 
 
 def measured_traffic(workload: str):
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summaries (profiles/pmc_traffic_*.md), or None."""
+    """HBM bytes per launch of the dominant (gate/up) kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summaries (the JSON blocks of
+    profiles/pmc_*.md), or None."""
     import glob
     import re
 
     here = os.path.dirname(os.path.abspath(__file__))
-    for path in sorted(glob.glob(os.path.join(here, "profiles", "pmc_traffic_*.md"))):
+    for path in sorted(glob.glob(os.path.join(here, "profiles", "pmc_*.md"))):
         with open(path) as f:
             text = f.read()
         for block in re.findall(r"```json\n(.*?)\n```", text, re.S):
@@ -350,11 +394,17 @@ def compact(name, rep):
            "gateup_us": round(ru["us_per_launch"], 2), "gateup_frac": round(ru["frac"], 4)}
     if "down" in rep["stages_us"]:
         out["down_us"] = round(rep["stages_us"]["down"], 2)
+    traffic = measured_traffic(name)
+    if traffic is not None:
+        out["gateup_traffic"] = traffic  # HBM bytes per gate/up launch (rocprofv3 counters)
     return out
 
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "The design note on sharding describes how the MoE path would split over GPUs.",
@@ -365,6 +415,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         sys.exit(1)
+    if args.pmc_copy:
+        pmc_copy(args.pmc_copy)
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     from trifuse_amd import workload as wl
