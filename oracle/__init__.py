@@ -243,6 +243,39 @@ def moe_reference(x, idx, gates, w, tokens=None, residual=None, rm: float = 1.0,
     return out
 
 
+def moe_reference_full(x, idx, gates, w, residual=None, rm: float = 1.0, dtype: str = "bf16") -> np.ndarray:
+    """moe_reference for every token, expert by expert with fp64 matrix
+    products: the same arithmetic as orc_moe_reference (weights dequantised
+    exactly by orc_dequant_f64, h = silu(x.gate) * (x.up) and the expert
+    outputs unrounded, then sum_k g_k y_k in k order, times rm, plus the
+    residual), with each dot product summed in BLAS order instead of
+    sequentially, so it agrees with moe_reference to fp64 rounding."""
+    xf = st_to_f32(_u16(x), dtype).astype(np.float64)
+    T, H = xf.shape
+    idx = _i32(idx)
+    K = idx.shape[1]
+    g = np.asarray(gates, dtype=np.float32).astype(np.float64).reshape(T, K)
+    contrib = np.zeros((T, K, H), dtype=np.float64)
+    flat = idx.reshape(-1)
+    for e in np.unique(flat):
+        routes = np.nonzero(flat == e)[0]
+        t, k = routes // K, routes % K
+        wg = dequant_f64(w.gate_q[e], w.gate_s[e], w.gate_b[e], dtype=dtype)
+        wu = dequant_f64(w.up_q[e], w.up_s[e], w.up_b[e], dtype=dtype)
+        wd = dequant_f64(w.down_q[e], w.down_s[e], w.down_b[e], dtype=dtype)
+        xe = xf[t]
+        a = xe @ wg.T
+        h = a / (1.0 + np.exp(-a)) * (xe @ wu.T)
+        contrib[t, k] = h @ wd.T
+    out = np.zeros((T, H), dtype=np.float64)
+    for k in range(K):
+        out += g[:, k:k + 1] * contrib[:, k]
+    out *= float(np.float32(rm))
+    if residual is not None:
+        out += st_to_f32(_u16(residual), dtype).astype(np.float64)
+    return out
+
+
 def moe_block_cpu(x, w, route: str, router, router_bias=None, residual=None, rm: float = 1.0,
                   top_k: int = 8, threads: int = 0):
     """The MLX-semantics CPU block (host-core baseline). Returns (y bf16 bits,

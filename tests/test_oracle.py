@@ -341,6 +341,25 @@ def test_moe_reference_matches_independent_block(bits):
     np.testing.assert_allclose(sub, ref[[4, 1]], rtol=1e-10, atol=1e-10)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_moe_reference_full_matches_reference(bits):
+    """The per-expert BLAS form (used for every token at full sizes) equals
+    the sequential fp64 reference and the independent block to fp64 rounding."""
+    w = tiny_block(bits=bits)
+    x = bf(RNG.standard_normal((9, 128)))
+    idx = RNG.integers(0, 4, (9, 3)).astype(np.int32)
+    idx[2] = [1, 1, 3]  # a token routed twice to one expert
+    gates = RNG.random((9, 3)).astype(np.float32)
+    res = bf(RNG.standard_normal((9, 128)))
+    got = oracle.moe_reference_full(x, idx, gates, w, residual=res, rm=0.75)
+    np.testing.assert_allclose(got, oracle.moe_reference(x, idx, gates, w, residual=res, rm=0.75),
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got, np_block(x, idx, gates, w, residual=res, rm=0.75), rtol=1e-10, atol=1e-10)
+    # planted mistakes fail it
+    assert not np.allclose(got, np_block(x, idx, gates, w, residual=res, rm=0.75, swap_gate_up=True))
+    assert not np.allclose(got, oracle.moe_reference_full(x, idx, gates, w, rm=0.75))
+
+
 @pytest.mark.parametrize("route,bits", [("olmoe", 4), ("granite", 4), ("olmoe", 8)])
 def test_cpu_block_matches_reference(route, bits):
     E, H, I, K = 8, 256, 128, 2
