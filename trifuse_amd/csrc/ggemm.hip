@@ -11,7 +11,8 @@
 //     row per step) into registers, dequantises them (s*q+b in fp32,
 //     rounded to the storage dtype, bf16 or half) and writes them to LDS,
 //   * runs v_mfma_f32_32x32x16_bf16 (or _f16) on the two LDS tiles, each wave owning a
-//     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane).
+//     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane); 32-row blocks
+//     past the end of the expert's segment skip their fragment reads and MFMAs.
 //
 // Pipeline: two LDS stages for each operand. While the MFMAs of step k read
 // stage k%2, the activations of step k+1 are copied into stage (k+1)%2, the
@@ -301,29 +302,31 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   // MFMAs of one LDS stage (fragments of K sub-step ks+1 are read during the
   // MFMAs of ks); the dequantised next B step is written during sub-steps
   // 1..3, so its loads have had more than a step to arrive.
-  // LIVE = false (every row of the wave past the segment): the wave skips
-  // fragment reads and MFMAs, which frees its SIMD's matrix pipe for the
-  // other wave there, and only does its share of the loads and LDS writes.
-  auto compute = [&](auto live_tag, const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt,
+  // MBL = the wave's 32-row blocks that hold rows of the segment (0..MB): the
+  // wave reads A fragments and runs MFMAs for those blocks only. With MBL = 0
+  // (every row of the wave past the segment) it skips fragment reads and
+  // MFMAs altogether, which frees its SIMD's matrix pipe for the other wave
+  // there, and only does its share of the loads and LDS writes.
+  auto compute = [&](auto mbl_tag, const uint16_t* A, const uint16_t* Bs, const RawB<LB>& nxt,
                      uint16_t* nB) {
-    constexpr bool LIVE = decltype(live_tag)::value;
+    constexpr int MBL = decltype(mbl_tag)::value;
     op8_t<F16> af[2][MB], bfr[2][NB];
     auto frag = [&](int ks, int slot) {
       const int kc = ks * 2 + (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+      for (int i = 0; i < MBL; ++i)
         af[slot][i] = *reinterpret_cast<const op8_t<F16>*>(&A[swz(wm * C::WM + i * 32 + (lane & 31), kc)]);
 #pragma unroll
       for (int j = 0; j < NB; ++j)
         bfr[slot][j] = *reinterpret_cast<const op8_t<F16>*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
     };
-    if constexpr (LIVE) frag(0, 0);
+    if constexpr (MBL > 0) frag(0, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      if constexpr (LIVE) {
+      if constexpr (MBL > 0) {
         if (ks < 3) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
+        for (int i = 0; i < MBL; ++i)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
             acc[i][j] = mfma32<F16>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
@@ -348,25 +351,41 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
 #pragma unroll
   for (int w = 0; w < LB * 4; ++w) bstore_word(st0, sB0, w);
   step_end();
-  auto main_loop = [&](auto live_tag) {
+  auto main_loop = [&](auto mbl_tag) {
     for (int kt = 0; kt < KT; kt += 2) {
       a_copy(sA1, kt + 1);
       bload(st0, kt + 2);
       __builtin_amdgcn_sched_barrier(0);
-      compute(live_tag, sA0, sB0, st1, sB1);
+      compute(mbl_tag, sA0, sB0, st1, sB1);
       step_end();
       a_copy(sA0, kt + 2);
       bload(st1, kt + 3);
       __builtin_amdgcn_sched_barrier(0);
-      compute(live_tag, sA1, sB1, st0, sB0);
+      compute(mbl_tag, sA1, sB1, st0, sB0);
       step_end();
     }
   };
-  const bool wave_live = wm * C::WM < rows_valid;
-  if (wave_live)
-    main_loop(std::true_type{});
-  else
-    main_loop(std::false_type{});
+  // Live row blocks of this wave (wave-uniform), one compiled loop per count.
+  static_assert(MB == 2 || MB == 4, "row blocks per wave");
+  const int live_rows = rows_valid - wm * C::WM;
+  const int mbl = live_rows <= 0 ? 0 : min(MB, (live_rows + 31) / 32);
+  if (mbl == MB) {
+    main_loop(std::integral_constant<int, MB>{});
+  } else if constexpr (MB == 4) {
+    if (mbl == 3)
+      main_loop(std::integral_constant<int, 3>{});
+    else if (mbl == 2)
+      main_loop(std::integral_constant<int, 2>{});
+    else if (mbl == 1)
+      main_loop(std::integral_constant<int, 1>{});
+    else
+      main_loop(std::integral_constant<int, 0>{});
+  } else {
+    if (mbl == 1)
+      main_loop(std::integral_constant<int, 1>{});
+    else
+      main_loop(std::integral_constant<int, 0>{});
+  }
 
   // ---- epilogue ----
   // Private staging block of this wave: 32 rows x SROW bf16 inside one of the
