@@ -121,6 +121,16 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* ds
 #endif
 }
 
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1 (compile-time
+// iteration: every index into register arrays is a constant).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS_>
 struct GgCfg {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, BITS = BITS_;
@@ -321,21 +331,21 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
         bfr[slot][j] = *reinterpret_cast<const op8_t<F16>*>(&Bs[swz(brow[j] + (lane & 31), kc)]);
     };
     if constexpr (MBL > 0) frag(0, 0);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    static_for<0, 4>([&](auto kc_) {
+      constexpr int ks = decltype(kc_)::value;
       if constexpr (MBL > 0) {
-        if (ks < 3) frag(ks + 1, (ks + 1) & 1);
+        if constexpr (ks < 3) frag(ks + 1, (ks + 1) & 1);
 #pragma unroll
         for (int i = 0; i < MBL; ++i)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
             acc[i][j] = mfma32<F16>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
       }
-      if (ks >= 1) {
+      if constexpr (ks >= 1) {
 #pragma unroll
         for (int w = (ks - 1) * LB * 4 / 3; w < ks * LB * 4 / 3; ++w) bstore_word(nxt, nB, w);
       }
-    }
+    });
   };
   // End of a step: the barrier's release fence waits for this wave's LDS
   // writes (copies and dequantised B) and its outstanding weight loads; after
@@ -394,10 +404,12 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   stage += (wave >> 2) * 32 * C::SROW;
   constexpr int CPR = C::WCOLS / 8;             // 16-byte chunks per staged row
   const int col_base = MODE == kGgGateUp ? n0 + wn * (C::WN / 2) : n0 + wn * C::WN;
-#pragma unroll
-  for (int i = 0; i < MB; ++i) {
+  // Row blocks by compile-time index (a runtime loop with an early exit can
+  // leave acc dynamically indexed, and then in scratch memory).
+  static_for<0, MB>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
     const int r0 = wm * C::WM + i * 32;         // first tile row of this block
-    if (r0 >= rows_valid) break;
+    if (r0 >= rows_valid) return;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int rr = acc_row(v, lane);
@@ -424,7 +436,7 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
         *reinterpret_cast<uint4*>(&args.out[orow * args.N + n]) = v;
       }
     }
-  }
+  });
 }
 
 // Tile shapes (eight waves each): 256 x 256 (2 x 4 waves of 128 x 64) when
