@@ -9,7 +9,10 @@
 //     (buffer loads with an LDS destination),
 //   * loads BN packed weight rows (4-bit: 32 bytes, 8-bit: 64 bytes of each
 //     row per step) into registers, dequantises them (s*q+b in fp32,
-//     rounded to the storage dtype, bf16 or half) and writes them to LDS,
+//     rounded to the storage dtype, bf16 or half) and writes them to LDS;
+//     for inputs up to 2048 wide the scales and biases of the tile's rows
+//     are copied into LDS once per tile (coalesced) instead of being loaded
+//     per step as 2-byte values from 64 rows at a time,
 //   * runs v_mfma_f32_32x32x16_bf16 (or _f16) on the two LDS tiles, each wave owning a
 //     WM x WN sub-tile (WM*WN/64 fp32 accumulators per lane); 32-row blocks
 //     past the end of the expert's segment skip their fragment reads and MFMAs.
@@ -162,7 +165,11 @@ struct RawB {
   uint32_t s[LB], bias[LB];
 };
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS, bool F16>
+// Largest input width whose scales and biases a tile keeps in LDS (32 groups
+// per weight row); wider inputs load them per step with the packed codes.
+constexpr int kLdsScaleKin = 32 * BK;
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE, int BITS, bool F16, bool SL>
 __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgArgs args) {
   using C = GgCfg<BM_, BN_, WAVES_M_, WAVES_N_, MODE, BITS>;
   constexpr int CPR_B = C::CPR_B;
@@ -174,8 +181,14 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   __shared__ __attribute__((aligned(16))) uint16_t sA1[BM * BK];
   __shared__ __attribute__((aligned(16))) uint16_t sB0[BN * BK];
   __shared__ __attribute__((aligned(16))) uint16_t sB1[BN * BK];
-  __shared__ int s_tiles[65];
-  __shared__ int s_expert;
+  // SL: scales and biases of the tile's weight rows for the whole input
+  // width (up to 32 groups per row), copied once per tile.
+  __shared__ __attribute__((aligned(16))) uint16_t sSc[SL ? BN * 32 : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t sBi[SL ? BN * 32 : 8];
+  // The tile prefix and the expert index live in weight stage 1, which is
+  // first written after the prologue's barrier.
+  int* const s_tiles = reinterpret_cast<int*>(sB1);
+  int& s_expert = s_tiles[65];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -266,14 +279,66 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
     b_qoff[i] = ok ? (uint32_t)bn * qrow + (q % CPR_B) * 16 : kOob;
     b_soff[i] = ok ? (uint32_t)bn * srow : kOob;
   }
-  auto bload = [&](RawB<LB>& st, int kt) {
+
+  // SL: the tile's weight rows fall into HALVES contiguous row ranges of the
+  // scale and bias matrices (gate/up: BN/2 gate rows, then BN/2 up rows;
+  // otherwise BN rows of one matrix). Each range is copied into LDS in 1 KB
+  // pieces at a 1 KB-aligned offset (HS bytes apart), so the zeros or
+  // neighbouring rows that a partial last piece brings in land in padding.
+  // Rows past N read as zero. Per K step a thread then reads its row's scale
+  // and bias from LDS instead of two 2-byte loads from 64 different rows.
+  constexpr int HALVES = MODE == kGgGateUp ? 2 : 1;
+  constexpr int HROWS = BN / HALVES;
+  const int G = args.Kin / BK;
+  const int hbytes = HROWS * G * 2;
+  const int hs = (hbytes + 1023) & ~1023;
+  int sidx[LB];
+  if constexpr (SL) {
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      const tfm_affine& bm = h ? args.wb : args.wa;
+      const size_t ebase = (size_t)e * args.N;
+      const auto rs = gg_rsrc(static_cast<const char*>(bm.scales) + ebase * srow, (uint32_t)args.N * srow);
+      const auto rb = gg_rsrc(static_cast<const char*>(bm.biases) + ebase * srow, (uint32_t)args.N * srow);
+      const uint32_t g0 = (uint32_t)n0 * srow;
+      for (int c = wave; c * 1024 < hbytes; c += C::WAVES) {
+        lds_dma16(rs, sSc + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
+        lds_dma16(rb, sBi + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int r = (i * T + tid) / CPR_B;
+      sidx[i] = (r / HROWS) * (hs / 2) + (r % HROWS) * G;
+    }
+  }
+  // Packed codes of step kt (and, without SL, its scale and bias).
+  auto bload_q = [&](RawB<LB>& st, int kt) {
     const bool live = kt < KT;
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
       st.b[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[i] : rnull, b_qoff[i], kt * (BK * BITS / 8), 0));
-      st.s[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbs[i] : rnull, b_soff[i], kt * 2, 0);
-      st.bias[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbb[i] : rnull, b_soff[i], kt * 2, 0);
+      if constexpr (!SL) {
+        st.s[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbs[i] : rnull, b_soff[i], kt * 2, 0);
+        st.bias[i] = __builtin_amdgcn_raw_buffer_load_b16(live ? rbb[i] : rnull, b_soff[i], kt * 2, 0);
+      }
     }
+  };
+  // SL: scale and bias of step kt from LDS (steps past the end reuse the
+  // last group; their codes and activations are zero).
+  auto bload_sb = [&](RawB<LB>& st, int kt) {
+    if constexpr (SL) {
+      const int g = kt < KT ? kt : KT - 1;
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        st.s[i] = sSc[sidx[i] + g];
+        st.bias[i] = sBi[sidx[i] + g];
+      }
+    }
+  };
+  auto bload = [&](RawB<LB>& st, int kt) {
+    bload_q(st, kt);
+    bload_sb(st, kt);
   };
   // Word w (of LB*4) of the dequantised B step: 8 elements (one LDS chunk)
   // for 4-bit, 4 elements (half a chunk) for 8-bit.
@@ -356,8 +421,12 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   // both read from null buffers), which adds nothing.
   RawB<LB> st0, st1;
   a_copy(sA0, 0);
-  bload(st0, 0);
-  bload(st1, 1);
+  bload_q(st0, 0);
+  bload_q(st1, 1);
+  // SL: every wave's scale copies are complete and visible after this barrier
+  if constexpr (SL) __syncthreads();
+  bload_sb(st0, 0);
+  bload_sb(st1, 1);
 #pragma unroll
   for (int w = 0; w < LB * 4; ++w) bstore_word(st0, sB0, w);
   step_end();
@@ -470,8 +539,12 @@ template <int BM_, int BN_, int WAVES_M, int WAVES_N, int MODE, int BITS, bool F
 static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
   using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS>;
   const int NT = (a.N + C::OUT_COLS - 1) / C::OUT_COLS;
-  ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16>
-      <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+  if (a.Kin <= kLdsScaleKin)
+    ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, true>
+        <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+  else
+    ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, false>
+        <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
 }
 
 template <int MODE, int BITS, bool F16>
