@@ -511,6 +511,357 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
 // Tile shapes (eight waves each): 256 x 256 (2 x 4 waves of 128 x 64) when
 // the experts hold enough routes to fill 256-row tiles, 128 x 256 (2 x 4
 // waves of 64 x 64) otherwise. TFM_GGEMM_TILE=256 or 128 forces one of them.
+// ---------------------------------------------------------------------------
+// 4-bit weights with inputs up to 2048 wide, a multiple of 128: the weights
+// stay in registers.
+//
+// Tile: BM routed rows x 256 weight rows, eight waves. Wave w owns 32 weight
+// rows (gate/up: gate rows 16w..16w+15 and the same up rows; down and plain:
+// rows 32w..32w+31) for all BM rows, as 16 x 16 blocks of
+// v_mfma_f32_16x16x32_bf16 (or _f16): BM/16 row blocks x 2 column blocks,
+// 4 fp32 accumulators each per lane. A gate block and its up block sit in
+// the same lanes, so SwiGLU needs no exchange.
+//
+// Per super-step of 128 k (two quantisation groups):
+//   * the BM activation rows are copied into LDS (one of two stages);
+//   * lane l loads 16 contiguous bytes (32 codes) of each of its two weight
+//     rows: k = 32 (l / 16) .. + 31 of the super-step, which share one scale
+//     group. Word s of them (k = 32 (l / 16) + 8 s .. + 7) is dequantised
+//     into the B operand of sub-step s. The reduction order inside an MFMA is
+//     free, so the A operand of sub-step s for lane l is the same k range:
+//     LDS chunk 4 (l / 16) + s of the row;
+//   * one barrier, for the next stage's activations.
+// Every packed weight is dequantised exactly once per tile and never goes
+// through LDS; scales and biases of the tile's rows are copied into LDS once
+// per tile. Per 128 k a wave runs 4 x BM/8 MFMAs for one barrier, twice the
+// work per barrier of the kernel above.
+//
+// LDS: activation row r of a stage is 256 B (16 chunks of 16 B); chunk c is
+// stored in slot c ^ (r & 15), so the 16 lanes of one read pass (16
+// consecutive rows, one chunk) hit distinct bank groups.
+constexpr int BK2 = 128;
+
+__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c, std::false_type) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(f16x8_t a, f16x8_t b, f32x4_t c, std::true_type) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <int BM, int MODE, bool F16>
+__global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
+  constexpr int WAVES = 8, T = 512, BN = 256;
+  constexpr int MB = BM / 16;                     // 16-row blocks per wave
+  constexpr int OUT_COLS = MODE == kGgGateUp ? BN / 2 : BN;
+  constexpr int LA = BM / 32;                     // 4-row (1 KB) copies per wave per super-step
+  constexpr int SROW = 136;                       // epilogue staging row stride (128 columns + 16 B)
+  constexpr int HALF_ROWS = BM / 2;               // staged rows per activation stage
+  static_assert(BM == 128 || BM == 256, "tile rows");
+  static_assert(HALF_ROWS * SROW <= BM * BK2, "epilogue staging fits a stage");
+  using op_t = op8_t<F16>;
+  using f16tag = std::integral_constant<bool, F16>;
+
+  __shared__ __attribute__((aligned(16))) uint16_t sA0[BM * BK2];
+  __shared__ __attribute__((aligned(16))) uint16_t sA1[BM * BK2];
+  __shared__ __attribute__((aligned(16))) uint16_t sSc[BN * 32];
+  __shared__ __attribute__((aligned(16))) uint16_t sBi[BN * 32];
+  // Tile prefix and expert index: in activation stage 1, first written after
+  // the prologue's barrier.
+  int* const s_tiles = reinterpret_cast<int*>(sA1);
+  int& s_expert = s_tiles[65];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int E = args.g.E;
+
+  // M-tile prefix over experts and the XCD-aware tile choice (as in
+  // ggemm_kernel).
+  if (tid < 64) {
+    int t = 0;
+    if (tid < E) {
+      const int cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
+      t = (cnt + BM - 1) / BM;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(t, d, 64);
+      if (lane >= d) t += o;
+    }
+    s_tiles[tid + 1] = t;
+    if (tid == 0) s_tiles[0] = 0;
+  }
+  __syncthreads();
+  const int NT = (args.N + OUT_COLS - 1) / OUT_COLS;
+  const int mtiles = s_tiles[E];
+  const int64_t total = (int64_t)mtiles * NT;
+  const int xcd = blockIdx.x & 7;
+  const int64_t local = blockIdx.x >> 3;
+  const int64_t share = (total + 7) / 8;
+  const int64_t ti = xcd * share + local;
+  if (local >= share || ti >= total) return;
+  const int mt = (int)(ti / NT), nt = (int)(ti % NT);
+  if (tid < E && s_tiles[tid] <= mt && mt < s_tiles[tid + 1]) s_expert = tid;
+  __syncthreads();
+  const int e = s_expert;
+  const int seg0 = args.g.offsets[e], seg1 = args.g.offsets[e + 1];
+  const int m0 = seg0 + (mt - s_tiles[e]) * BM;
+  const int rows_valid = min(BM, seg1 - m0);
+  const int n0 = nt * OUT_COLS;
+  const int KT = args.Kin / BK2;
+  const int G = args.Kin / BK;                    // quantisation groups per row
+
+  // ---- activations: global -> LDS ----
+  // Copy i of wave w: rows 4 (LA w + i) .. + 3; lane l writes slot l % 16 of
+  // row 4 (LA w + i) + l / 16, which holds chunk (l % 16) ^ (row & 15).
+  const __amdgpu_buffer_rsrc_t ra = gg_rsrc(args.x, args.x_bytes);
+  const __amdgpu_buffer_rsrc_t rnull = gg_rsrc(args.x, 0);
+  uint32_t a_off[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int r = 4 * (LA * wave + i) + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    if (r < rows_valid) {
+      const int64_t src = MODE == kGgDown ? (int64_t)(m0 + r) : route_row(args.rm, m0 + r);
+      a_off[i] = (uint32_t)((src * args.Kin + c * 8) * 2);
+    } else {
+      a_off[i] = kOob;
+    }
+  }
+  auto a_copy = [&](uint16_t* dst, int kt) {
+    const __amdgpu_buffer_rsrc_t r = kt < KT ? ra : rnull;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) lds_dma16(r, dst + 4 * (LA * wave + i) * BK2, a_off[i], kt * BK2 * 2);
+  };
+  // Copy i alone (the main loop spreads the copies over a super-step).
+  auto a_copy1 = [&](uint16_t* dst, int kt, auto i_) {
+    constexpr int i = decltype(i_)::value;
+    const __amdgpu_buffer_rsrc_t r = kt < KT ? ra : rnull;
+    lds_dma16(r, dst + 4 * (LA * wave + i) * BK2, a_off[i], kt * BK2 * 2);
+  };
+
+  // ---- weights ----
+  const int g4 = lane >> 4;                       // k quarter of the super-step
+  const uint32_t qrow = (uint32_t)args.Kin / 2, srow = (uint32_t)G * 2;
+  __amdgpu_buffer_rsrc_t rbq[2];
+  uint32_t b_qoff[2];
+  int trow[2];                                    // weight row within the tile (0..255)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const tfm_affine& bm = (MODE == kGgGateUp && j == 1) ? args.wb : args.wa;
+    trow[j] = MODE == kGgGateUp ? j * 128 + 16 * wave + (lane & 15) : 32 * wave + 16 * j + (lane & 15);
+    const int bn = MODE == kGgGateUp ? n0 + 16 * wave + (lane & 15) : n0 + 32 * wave + 16 * j + (lane & 15);
+    rbq[j] = gg_rsrc(reinterpret_cast<const char*>(bm.q) + (size_t)e * args.N * qrow, (uint32_t)args.N * qrow);
+    b_qoff[j] = bn < args.N ? (uint32_t)bn * qrow + 16u * g4 : kOob;
+  }
+  auto bload = [&](uint4* raw, int kt) {
+    const bool live = kt < KT;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      raw[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[j] : rnull, b_qoff[j], kt * 64, 0));
+  };
+
+  // Scales and biases of the tile's rows, copied once (as in ggemm_kernel's
+  // SL path): HALVES contiguous row ranges, each at a 1 KB-aligned offset.
+  constexpr int HALVES = MODE == kGgGateUp ? 2 : 1;
+  constexpr int HROWS = BN / HALVES;
+  const int hbytes = HROWS * G * 2;
+  const int hs = (hbytes + 1023) & ~1023;
+#pragma unroll
+  for (int h = 0; h < HALVES; ++h) {
+    const tfm_affine& bm = h ? args.wb : args.wa;
+    const size_t ebase = (size_t)e * args.N;
+    const auto rs = gg_rsrc(static_cast<const char*>(bm.scales) + ebase * srow, (uint32_t)args.N * srow);
+    const auto rb = gg_rsrc(static_cast<const char*>(bm.biases) + ebase * srow, (uint32_t)args.N * srow);
+    const uint32_t g0 = (uint32_t)n0 * srow;
+    for (int c = wave; c * 1024 < hbytes; c += WAVES) {
+      lds_dma16(rs, sSc + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
+      lds_dma16(rb, sBi + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
+    }
+  }
+  int sidx[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) sidx[j] = (trow[j] / HROWS) * (hs / 2) + (trow[j] % HROWS) * G;
+  // scale and bias of super-step kt for both rows (past the end: last group)
+  auto sb_read = [&](float* sc, float* bi, int kt) {
+    int g = 2 * kt + (g4 >> 1);
+    g = g < G ? g : G - 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      sc[j] = st2f<F16>(sSc[sidx[j] + g]);
+      bi[j] = st2f<F16>(sBi[sidx[j] + g]);
+    }
+  };
+  auto deq = [&](op_t* b, const uint4* raw, const float* sc, const float* bi, int s) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[j] = __builtin_bit_cast(op_t, dequant_word<F16>(word_of(raw[j], s), sc[j], bi[j]));
+  };
+
+  f32x4_t acc[MB][2];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // One super-step on activation stage A: sub-step s runs the MFMAs of the
+  // MBL live row blocks with B operand b (word s) and dequantises the B
+  // operand of the next sub-step (word s + 1, or word 0 of the next
+  // super-step's raw weights). The (sub-step, row block) pairs run as one
+  // compile-time sequence with the A fragment of pair q + D read while pair
+  // q computes (a ring of D + 1 fragments); the scheduler is asked for the
+  // first D reads, then per pair two MFMAs, the read D pairs ahead and three
+  // VALU instructions. The LA activation copies of the next super-step (into
+  // stage An) are issued one every STEP pairs over the first half of the
+  // sequence: issued together they would hold the wave at the address unit,
+  // with no MFMAs issued, for most of a thousand cycles.
+  // Fragment address of row block i, sub-step s: the lane's byte offset
+  // (row lane % 16, slot (4 g4) ^ (lane % 16)) XOR 16 s, plus 4096 i. The
+  // lane offset is made opaque per super-step so that the four per-sub-step
+  // addresses are formed there instead of being held across the loop.
+  const uint32_t a_lane = (uint32_t)((lane & 15) * BK2 * 2 + (((4 * g4) ^ (lane & 15)) << 4));
+  auto compute = [&](auto mbl_tag, const uint16_t* A, op_t* b, const uint4* rc, const float* sc,
+                     const float* bic, const uint4* rn, const float* sn, const float* bin, uint16_t* An,
+                     int ktn) __attribute__((always_inline)) {
+    constexpr int MBL = decltype(mbl_tag)::value;
+    constexpr int NQ = 4 * MBL, D = 3, R = D + 1;
+    constexpr int STEP = NQ / (2 * LA) > 0 ? NQ / (2 * LA) : 1;
+    static_assert(STEP * (LA - 1) < NQ, "every copy is issued");
+    op_t af[R];
+    uint32_t nbw[2][4];                           // next B operand, packed pairs
+    uint32_t lo[2], hi[2];                        // nibble bytes of the word being dequantised
+    float f[16];
+    uint32_t al = a_lane;
+    asm volatile("" : "+v"(al));
+    const char* const Ab = reinterpret_cast<const char*>(A);
+    auto rd = [&](auto q_) {
+      constexpr int q = decltype(q_)::value, s = q / MBL, i = q % MBL;
+      af[q % R] = *reinterpret_cast<const op_t*>(Ab + (al ^ (16u * s)) + 16 * BK2 * 2 * i);
+    };
+    static_for<0, D>([&](auto q_) { rd(q_); });
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NQ>([&](auto q_) {
+      constexpr int q = decltype(q_)::value, s = q / MBL, i = q % MBL;
+      if constexpr (q % STEP == 0 && q / STEP < LA) a_copy1(An, ktn, std::integral_constant<int, q / STEP>{});
+      if constexpr (q + D < NQ) rd(std::integral_constant<int, q + D>{});
+      acc[i][0] = mfma16(af[q % R], b[0], acc[i][0], f16tag{});
+      acc[i][1] = mfma16(af[q % R], b[1], acc[i][1], f16tag{});
+      // Slice of the next sub-step's B operand: codes c0..c1-1 of the 16
+      // (code c: row j = c / 8, element c % 8 of word s + 1, or word 0 of
+      // the next super-step's raw weights).
+      constexpr int c0 = 16 * i / MBL, c1 = 16 * (i + 1) / MBL;
+      static_for<c0, c1>([&](auto c_) {
+        constexpr int c = decltype(c_)::value, j = c / 8, el = c % 8;
+        const uint32_t* rw = s < 3 ? reinterpret_cast<const uint32_t*>(&rc[j]) : reinterpret_cast<const uint32_t*>(&rn[j]);
+        const float scj = s < 3 ? sc[j] : sn[j], bij = s < 3 ? bic[j] : bin[j];
+        if constexpr (el == 0) {
+          const uint32_t w = rw[s < 3 ? s + 1 : 0];
+          lo[j] = w & 0x0f0f0f0fu;
+          hi[j] = (w >> 4) & 0x0f0f0f0fu;
+          asm("" : "+v"(lo[j]));
+          asm("" : "+v"(hi[j]));
+        }
+        const uint32_t src = (el & 1) ? hi[j] : lo[j];
+        f[c] = __builtin_fmaf(scj, (float)((src >> (8 * (el >> 1))) & 0xffu), bij);
+        if constexpr (el & 1) nbw[j][el >> 1] = pack_st2<F16>(f[c - 1], f[c]);
+      });
+      if constexpr (i == MBL - 1) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          b[j] = __builtin_bit_cast(op_t, make_uint4(nbw[j][0], nbw[j][1], nbw[j][2], nbw[j][3]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // ---- prologue ----
+  uint4 r0[2], r1[2];
+  float sc0[2], bi0[2], sc1[2], bi1[2];
+  op_t bop[2];
+  a_copy(sA0, 0);
+  bload(r0, 0);
+  __syncthreads();  // scale copies and stage 0 complete and visible
+  sb_read(sc0, bi0, 0);
+  deq(bop, r0, sc0, bi0, 0);
+
+  // Super-step S: load the raw weights of S+1 and read its scales, compute
+  // (copying S+1 into the other stage on the way), barrier. With an odd
+  // count the loop runs one more super-step on zero activations.
+  auto main_loop = [&](auto mbl_tag) {
+    for (int kt = 0; kt < KT; kt += 2) {
+      bload(r1, kt + 1);
+      sb_read(sc1, bi1, kt + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(mbl_tag, sA0, bop, r0, sc0, bi0, r1, sc1, bi1, sA1, kt + 1);
+      __syncthreads();
+      bload(r0, kt + 2);
+      sb_read(sc0, bi0, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(mbl_tag, sA1, bop, r1, sc1, bi1, r0, sc0, bi0, sA0, kt + 2);
+      __syncthreads();
+    }
+  };
+  // Live row blocks (uniform over the workgroup), in steps of four.
+  const int live = min(MB, ((rows_valid + 63) / 64) * 4);
+  if constexpr (MB == 16) {
+    if (live == 16)
+      main_loop(std::integral_constant<int, 16>{});
+    else if (live == 12)
+      main_loop(std::integral_constant<int, 12>{});
+    else if (live == 8)
+      main_loop(std::integral_constant<int, 8>{});
+    else
+      main_loop(std::integral_constant<int, 4>{});
+  } else {
+    if (live == 8)
+      main_loop(std::integral_constant<int, 8>{});
+    else
+      main_loop(std::integral_constant<int, 4>{});
+  }
+
+  // ---- epilogue ----
+  // Rows staged row-major, 128 columns per pass (the first BM/2 rows in
+  // stage 0, the rest in stage 1), then written as 16-byte row pieces. Gate/up: one
+  // pass (wave w holds columns 16w..16w+15 after SwiGLU); down and plain:
+  // two passes, waves 4p..4p+3 staging columns 128p..128p+127.
+  constexpr int PASSES = MODE == kGgGateUp ? 1 : 2;
+  static_for<0, PASSES>([&](auto p_) {
+    constexpr int p = decltype(p_)::value;
+    if (p > 0) __syncthreads();  // the previous pass's reads are done
+    const bool mine = MODE == kGgGateUp || (wave >> 2) == p;
+    if (mine) {
+      static_for<0, MB>([&](auto i_) {
+        constexpr int i = decltype(i_)::value;
+        if (16 * i >= rows_valid) return;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * i + 4 * g4 + v;
+          uint16_t* st = (row < HALF_ROWS ? sA0 : sA1) + (row % HALF_ROWS) * SROW;
+          if constexpr (MODE == kGgGateUp) {
+            st[16 * wave + (lane & 15)] = f2st<F16>(swiglu(acc[i][0][v], acc[i][1][v]));
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) st[32 * (wave & 3) + 16 * j + (lane & 15)] = f2st<F16>(acc[i][j][v]);
+          }
+        }
+      });
+    }
+    __syncthreads();
+    const int part = tid & 15;
+    const int n = n0 + 128 * p + part * 8;
+#pragma unroll
+    for (int r0i = 0; r0i < BM; r0i += 32) {
+      const int row = r0i + (tid >> 4);
+      if (row < rows_valid && n < args.N) {
+        const uint16_t* st = (row < HALF_ROWS ? sA0 : sA1) + (row % HALF_ROWS) * SROW;
+        const uint4 v = *reinterpret_cast<const uint4*>(&st[part * 8]);
+        const int j = m0 + row;
+        const int64_t orow = MODE == kGgPlain ? (int64_t)args.rm.order[j] : (int64_t)j;
+        *reinterpret_cast<uint4*>(&args.out[orow * args.N + n]) = v;
+      }
+    }
+  });
+}
+
 static int tile_override() {
   static int v = [] {
     const char* s = std::getenv("TFM_GGEMM_TILE");
@@ -547,8 +898,28 @@ static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) 
         <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
 }
 
+// 4-bit weights, inputs up to 2048 wide and a multiple of 128: weights in
+// registers (ggemm_wr_kernel); otherwise ggemm_kernel.
+template <int BM, int MODE, bool F16>
+static void launch_wr(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  constexpr int OUT_COLS = MODE == kGgGateUp ? 128 : 256;
+  const int NT = (a.N + OUT_COLS - 1) / OUT_COLS;
+  ggemm_wr_kernel<BM, MODE, F16><<<grid_for(n_routes, E, BM, NT), 512, 0, s>>>(a);
+}
+
 template <int MODE, int BITS, bool F16>
 static void launch_tile(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+#ifndef GG_NO_WR
+  if constexpr (BITS == 4) {
+    if (a.Kin <= kLdsScaleKin && a.Kin % BK2 == 0) {
+      if (use_tall(n_routes, E))
+        launch_wr<256, MODE, F16>(a, n_routes, E, s);
+      else
+        launch_wr<128, MODE, F16>(a, n_routes, E, s);
+      return;
+    }
+  }
+#endif
   if (use_tall(n_routes, E))
     launch_one<256, 256, 2, 4, MODE, BITS, F16>(a, n_routes, E, s);
   else
