@@ -565,42 +565,66 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
   __shared__ __attribute__((aligned(16))) uint16_t sA1[BM * BK2];
   __shared__ __attribute__((aligned(16))) uint16_t sSc[BN * 32];
   __shared__ __attribute__((aligned(16))) uint16_t sBi[BN * 32];
-  // Tile prefix and expert index: in activation stage 1, first written after
-  // the prologue's barrier.
+  // Tile prefix, XCD bounds and expert index: in activation stage 1, first
+  // written after the prologue's barrier.
   int* const s_tiles = reinterpret_cast<int*>(sA1);
+  int* const s_bound = s_tiles + 66;
   int& s_expert = s_tiles[65];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int E = args.g.E;
+  const int NT = (args.N + OUT_COLS - 1) / OUT_COLS;
+  const int xcd = blockIdx.x & 7;
+  const int local = blockIdx.x >> 3;
 
-  // M-tile prefix over experts and the XCD-aware tile choice (as in
-  // ggemm_kernel).
+  // Tiles in m-major order (experts in order, their m-tiles, n-tiles
+  // innermost). Workgroups are dispatched round-robin over the 8 XCDs; XCD
+  // x takes a contiguous run of the order (its n-tiles and neighbouring
+  // m-tiles share activations and weights in its L2) holding about 1/8 of
+  // the estimated work. With 256-row tiles a tile costs about 13 + (live
+  // 16-row blocks) units (measured: 23.6 + 1.85 x blocks microseconds at
+  // 4096 tokens), so runs of short tiles are longer; 128-row tiles cost
+  // about the same whatever their rows, and count one unit each.
+  constexpr bool BAL = BM == 256;
+  constexpr int CF = BAL ? 13 + MB : 1;
   if (tid < 64) {
-    int t = 0;
-    if (tid < E) {
-      const int cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
-      t = (cnt + BM - 1) / BM;
-    }
+    int cnt = 0;
+    if (tid < E) cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
+    const int full = cnt / BM, part = cnt % BM;
+    const int cp = part > 0 ? (BAL ? 13 + min(MB, ((part + 63) / 64) * 4) : 1) : 0;
+    const int mt_e = full + (part > 0 ? 1 : 0);
+    const int cost_e = NT * (full * CF + cp);
+    int mt_i = mt_e, cost_i = cost_e;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(t, d, 64);
-      if (lane >= d) t += o;
+      const int o1 = __shfl_up(mt_i, d, 64), o2 = __shfl_up(cost_i, d, 64);
+      if (lane >= d) {
+        mt_i += o1;
+        cost_i += o2;
+      }
     }
-    s_tiles[tid + 1] = t;
+    s_tiles[tid + 1] = mt_i;
     if (tid == 0) s_tiles[0] = 0;
+    const int W = __shfl(cost_i, 63, 64);
+    // bound k: tiles whose start lies below target (xcd + k) W / 8
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int T = (int)(((int64_t)(xcd + k) * W) / 8);
+      if (tid == 0) s_bound[k] = 0;
+      const int pc = cost_i - cost_e;
+      if (tid < E && pc < T && T <= cost_i) {
+        const int rel = T - pc, fc = full * NT * CF;
+        const int c = rel <= fc ? (rel + CF - 1) / CF : full * NT + (rel - fc + cp - 1) / cp;
+        s_bound[k] = (mt_i - mt_e) * NT + c;
+      }
+    }
   }
   __syncthreads();
-  const int NT = (args.N + OUT_COLS - 1) / OUT_COLS;
-  const int mtiles = s_tiles[E];
-  const int64_t total = (int64_t)mtiles * NT;
-  const int xcd = blockIdx.x & 7;
-  const int64_t local = blockIdx.x >> 3;
-  const int64_t share = (total + 7) / 8;
-  const int64_t ti = xcd * share + local;
-  if (local >= share || ti >= total) return;
-  const int mt = (int)(ti / NT), nt = (int)(ti % NT);
+  const int ti = s_bound[0] + local;
+  if (ti >= s_bound[1]) return;
+  const int mt = ti / NT, nt = ti % NT;
   if (tid < E && s_tiles[tid] <= mt && mt < s_tiles[tid + 1]) s_expert = tid;
   __syncthreads();
   const int e = s_expert;
@@ -904,7 +928,12 @@ template <int BM, int MODE, bool F16>
 static void launch_wr(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
   constexpr int OUT_COLS = MODE == kGgGateUp ? 128 : 256;
   const int NT = (a.N + OUT_COLS - 1) / OUT_COLS;
-  ggemm_wr_kernel<BM, MODE, F16><<<grid_for(n_routes, E, BM, NT), 512, 0, s>>>(a);
+  // With 256-row tiles an XCD's run of cheap tiles holds more tiles than an
+  // even share: at most share x 29 / 17 + 2 (full tile 29 units, cheapest
+  // 17); workgroups past their XCD's run exit at once.
+  unsigned grid = grid_for(n_routes, E, BM, NT);
+  if (BM == 256) grid = ((grid / 8 * 29 + 16) / 17 + 2) * 8;
+  ggemm_wr_kernel<BM, MODE, F16><<<grid, 512, 0, s>>>(a);
 }
 
 template <int MODE, int BITS, bool F16>
