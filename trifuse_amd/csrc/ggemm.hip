@@ -636,14 +636,15 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
   const int G = args.Kin / BK;                    // quantisation groups per row
 
   // ---- activations: global -> LDS ----
-  // Copy i of wave w: rows 4 (LA w + i) .. + 3; lane l writes slot l % 16 of
-  // row 4 (LA w + i) + l / 16, which holds chunk (l % 16) ^ (row & 15).
+  // Copy i of wave w: rows 4 (8 i + w) .. + 3 (copy i of all waves together:
+  // rows 32 i .. 32 i + 31); lane l writes slot l % 16 of row
+  // 4 (8 i + w) + l / 16, which holds chunk (l % 16) ^ (row & 15).
   const __amdgpu_buffer_rsrc_t ra = gg_rsrc(args.x, args.x_bytes);
   const __amdgpu_buffer_rsrc_t rnull = gg_rsrc(args.x, 0);
   uint32_t a_off[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int r = 4 * (LA * wave + i) + (lane >> 4);
+    const int r = 4 * (WAVES * i + wave) + (lane >> 4);
     const int c = (lane & 15) ^ (r & 15);
     if (r < rows_valid) {
       const int64_t src = MODE == kGgDown ? (int64_t)(m0 + r) : route_row(args.rm, m0 + r);
@@ -655,13 +656,13 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
   auto a_copy = [&](uint16_t* dst, int kt) {
     const __amdgpu_buffer_rsrc_t r = kt < KT ? ra : rnull;
 #pragma unroll
-    for (int i = 0; i < LA; ++i) lds_dma16(r, dst + 4 * (LA * wave + i) * BK2, a_off[i], kt * BK2 * 2);
+    for (int i = 0; i < LA; ++i) lds_dma16(r, dst + 4 * (WAVES * i + wave) * BK2, a_off[i], kt * BK2 * 2);
   };
   // Copy i alone (the main loop spreads the copies over a super-step).
   auto a_copy1 = [&](uint16_t* dst, int kt, auto i_) {
     constexpr int i = decltype(i_)::value;
     const __amdgpu_buffer_rsrc_t r = kt < KT ? ra : rnull;
-    lds_dma16(r, dst + 4 * (LA * wave + i) * BK2, a_off[i], kt * BK2 * 2);
+    lds_dma16(r, dst + 4 * (WAVES * i + wave) * BK2, a_off[i], kt * BK2 * 2);
   };
 
   // ---- weights ----
@@ -734,10 +735,11 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
   // compile-time sequence with the A fragment of pair q + D read while pair
   // q computes (a ring of D + 1 fragments); the scheduler is asked for the
   // first D reads, then per pair two MFMAs, the read D pairs ahead and three
-  // VALU instructions. The LA activation copies of the next super-step (into
+  // VALU instructions. The activation copies of the next super-step (into
   // stage An) are issued one every STEP pairs over the first half of the
   // sequence: issued together they would hold the wave at the address unit,
-  // with no MFMAs issued, for most of a thousand cycles.
+  // with no MFMAs issued, for most of a thousand cycles. Only the NC copies
+  // of rows below 16 MBL are issued: the other rows are never read.
   // Fragment address of row block i, sub-step s: the lane's byte offset
   // (row lane % 16, slot (4 g4) ^ (lane % 16)) XOR 16 s, plus 4096 i. The
   // lane offset is made opaque per super-step so that the four per-sub-step
@@ -748,8 +750,9 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
                      int ktn) __attribute__((always_inline)) {
     constexpr int MBL = decltype(mbl_tag)::value;
     constexpr int NQ = 4 * MBL, D = 3, R = D + 1;
-    constexpr int STEP = NQ / (2 * LA) > 0 ? NQ / (2 * LA) : 1;
-    static_assert(STEP * (LA - 1) < NQ, "every copy is issued");
+    constexpr int NC = (16 * MBL + 31) / 32 < LA ? (16 * MBL + 31) / 32 : LA;
+    constexpr int STEP = NQ / (2 * NC) > 0 ? NQ / (2 * NC) : 1;
+    static_assert(STEP * (NC - 1) < NQ, "every copy is issued");
     op_t af[R];
     uint32_t nbw[2][4];                           // next B operand, packed pairs
     uint32_t lo[2], hi[2];                        // nibble bytes of the word being dequantised
@@ -765,7 +768,7 @@ __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NQ>([&](auto q_) {
       constexpr int q = decltype(q_)::value, s = q / MBL, i = q % MBL;
-      if constexpr (q % STEP == 0 && q / STEP < LA) a_copy1(An, ktn, std::integral_constant<int, q / STEP>{});
+      if constexpr (q % STEP == 0 && q / STEP < NC) a_copy1(An, ktn, std::integral_constant<int, q / STEP>{});
       if constexpr (q + D < NQ) rd(std::integral_constant<int, q + D>{});
       acc[i][0] = mfma16(af[q % R], b[0], acc[i][0], f16tag{});
       acc[i][1] = mfma16(af[q % R], b[1], acc[i][1], f16tag{});
