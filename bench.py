@@ -285,7 +285,11 @@ def dominant_roofline(r: Runner, stages):
                 "us_per_launch": st["us_per_launch"]}
     flops = wl.gemm_flops(g, T * g.top_k, "gateup")
     achieved = flops / dur_s / 1e12
-    return {"kernel": "ggemm_kernel<gateup>", "bound": "mfma", "achieved": achieved,
+    # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
+    # weights-in-registers kernel, everything else the LDS-dequant one
+    wr = r.wl.bits == 4 and H <= 2048 and H % 128 == 0
+    return {"kernel": "ggemm_wr_kernel<gateup>" if wr else "ggemm_kernel<gateup>", "bound": "mfma",
+            "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
             "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}
 
