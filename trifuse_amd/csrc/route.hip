@@ -78,14 +78,16 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
 }
 
 // Prefill routing in one pass: router linear, top-k and the chunk histogram
-// for the grouping. A workgroup takes kTopkTokensPerBlock (4) tokens: every
-// wave keeps their x rows in registers and computes the logits of one
-// quarter of the experts, streaming those router rows (the next one loading
+// for the grouping. A workgroup takes kTopkTokensPerBlock (4) tokens with W
+// waves: every wave keeps their x rows in registers and computes the logits
+// of 1/W of the experts, streaming those router rows (the next one loading
 // while the current one is used), each logit exactly as router_logits_kernel
-// computes it. Then wave t ranks token t from the logits in LDS with the same
-// wave-level ranking as topk_kernel.
-template <int C, int ROUTE, bool F16>
-__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __restrict__ x,
+// computes it. Then wave t < 4 ranks token t from the logits in LDS with the
+// same wave-level ranking as topk_kernel. Few tokens take W = 8 (each wave
+// waits on a chain of E/8 router-row loads instead of E/4: 512 tokens
+// 21 -> 16 us); many take W = 4, two workgroups per compute unit.
+template <int C, int ROUTE, bool F16, int W>
+__global__ __launch_bounds__(W * 64) void router_topk_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const float* __restrict__ bias, int T,
                                                           int H, int E, int K,
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
       if (lane == 63) s_logit[t][e] = f2st<F16>(bias ? s + be : s);
     }
   };
-  const int epw = (E + 3) / 4;
+  const int epw = (E + W - 1) / W;
   const int e0 = wave * epw, e1 = min(E, e0 + epw);
   if (e0 < e1) {  // wave-uniform
     uint4 ra[C / 8], rb[C / 8];
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __rest
   }
   __syncthreads();  // every expert's logits of the block's tokens are in LDS
   const int tok = t0 + wave;
-  if (tok < T) {  // wave-uniform
+  if (wave < TB && tok < T) {  // wave-uniform
     const uint16_t* row = &s_logit[wave][0];
     if (logits_out && lane < E) logits_out[(int64_t)tok * E + lane] = row[lane];
     float g;
@@ -186,12 +188,22 @@ static void launch_router_topk_c(int route_kind, const uint16_t* x, const uint16
                                  float* gates_f32, int32_t* hist, uint16_t* logits_out,
                                  hipStream_t s) {
   const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
-  if (route_kind == TFM_ROUTE_OLMOE)
-    router_topk_kernel<C, TFM_ROUTE_OLMOE, F16><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx,
-                                                                      gates_f32, hist, logits_out);
-  else
-    router_topk_kernel<C, TFM_ROUTE_GRANITE, F16><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx,
-                                                                        gates_f32, hist, logits_out);
+  const bool few = blocks < 512;  // under 2048 tokens: eight waves per workgroup
+  if (route_kind == TFM_ROUTE_OLMOE) {
+    if (few)
+      router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 8><<<blocks, 512, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                          hist, logits_out);
+    else
+      router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 4><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                          hist, logits_out);
+  } else {
+    if (few)
+      router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 8><<<blocks, 512, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                            hist, logits_out);
+    else
+      router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 4><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
+                                                                            hist, logits_out);
+  }
 }
 
 template <bool F16>
