@@ -277,11 +277,18 @@ def dominant_roofline(r: Runner, stages):
     if r.wl.name in DECODE:
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
-        achieved = per_launch / dur_s / 1e9
+        # At one or two tokens (T*K <= 16) the gate/up kernel also copies the
+        # routed experts' down Q/S/B from HBM into L2 for the fused
+        # down+combine kernel: those bytes are moved by this kernel.
+        dn_bytes_expert = H * I * r.wl.bits // 8 + 2 * (H * I // 64) * 2
+        prefetch = (sum(U) / len(U) * dn_bytes_expert) if (streaming and T <= 2 and T * g.top_k <= 16) else 0.0
+        achieved = (per_launch + prefetch) / dur_s / 1e9
         return {"kernel": "ds_gateup_kernel" if streaming else "ggemm_kernel<gateup>",
                 "bound": "hbm", "achieved": achieved,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                "traffic": None, "alg_bytes_per_launch": per_launch,
+                "traffic": None, "alg_bytes_per_launch": per_launch + prefetch,
+                "prefetch_bytes_per_launch": prefetch,
+                "frac_gateup_bytes_only": per_launch / dur_s / 1e9 / HBM_PEAK_GBS,
                 "us_per_launch": st["us_per_launch"]}
     flops = wl.gemm_flops(g, T * g.top_k, "gateup")
     achieved = flops / dur_s / 1e12

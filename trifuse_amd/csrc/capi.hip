@@ -256,7 +256,7 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     {
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_ds_gateup(f16, g.bits, kDsGivenRoutes, x, nullptr, const_cast<int32_t*>(idx), const_cast<float*>(gates),
-                       (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s);
+                       (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s, &w->down);
     }
     if (decode_small((int)T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
@@ -615,7 +615,7 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
       // Top-k and grouping run in this kernel's prologue.
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_ds_gateup(f16, g.bits, g.route, static_cast<const uint16_t*>(x), ws.logits, ws.idx, ws.gates, T, K, E, H,
-                       I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s);
+                       I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s, &weights->down);
     }
     const int max_active = (int)(R < E ? R : E);
     if (decode_small(T, K)) {

@@ -550,7 +550,7 @@ __device__ __forceinline__ f32x4_t mfma16(f16x8_t a, f16x8_t b, f32x4_t c, std::
 
 template <int BM, int MODE, bool F16>
 __global__ __launch_bounds__(512, 1) void ggemm_wr_kernel(GgArgs args) {
-  constexpr int WAVES = 8, T = 512, BN = 256;
+  constexpr int WAVES = 8, BN = 256;
   constexpr int MB = BM / 16;                     // 16-row blocks per wave
   constexpr int OUT_COLS = MODE == kGgGateUp ? BN / 2 : BN;
   constexpr int LA = BM / 32;                     // 4-row (1 KB) copies per wave per super-step

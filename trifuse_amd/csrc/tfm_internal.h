@@ -122,7 +122,8 @@ constexpr int kDsGivenRoutes = 2;
   bool decode_stream_fits(int T, int K, int E, int H, int I);                                             \
   void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,  \
                         int T, int K, int E, int H, int I, const tfm_affine& gate, const tfm_affine& up,  \
-                        const Grouping& g, uint32_t* status, uint16_t* h, hipStream_t s);                 \
+                        const Grouping& g, uint32_t* status, uint16_t* h, const tfm_affine* pf_down,      \
+                        hipStream_t s);                                                                   \
   void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,      \
                       const Grouping& g, float* P, hipStream_t s);                                        \
   bool decode_small(int T, int K);                                                                        \
@@ -152,8 +153,8 @@ inline bool decode_small(int T, int K) { return ds_bf16::decode_small(T, K); }
 inline void launch_ds_gateup(bool f16, int bits, int mode, const uint16_t* x, const uint16_t* logits,
                              int32_t* idx, float* gates, int T, int K, int E, int H, int I,
                              const tfm_affine& gate, const tfm_affine& up, const Grouping& g,
-                             uint32_t* status, uint16_t* h, hipStream_t s) {
-  TFM_DS_PICK(f16, bits, launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, s));
+                             uint32_t* status, uint16_t* h, hipStream_t s, const tfm_affine* pf_down = nullptr) {
+  TFM_DS_PICK(f16, bits, launch_ds_gateup(mode, x, logits, idx, gates, T, K, E, H, I, gate, up, g, status, h, pf_down, s));
 }
 inline void launch_ds_down(bool f16, int bits, const uint16_t* hsorted, int H, int I, int max_active,
                            const tfm_affine& down, const Grouping& g, float* P, hipStream_t s) {
