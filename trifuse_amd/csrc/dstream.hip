@@ -464,8 +464,7 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
   // T*K routes itself (a few hundred VALU operations, cheaper than one more
   // dependent kernel launch) and workgroup 0 publishes the result for the
   // down projection and the combine. The first items' weights go out as soon
-  // as the grouping is known; the x rows are permuted into dot2 pair order
-  // and stored while those weights are in flight.
+  // as the grouping is known.
   uint4 xr[XCH][4];
 #pragma unroll
   for (int u = 0; u < XCH; ++u) {
@@ -476,14 +475,45 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
       for (int v = 0; v < 4; ++v) xr[u][v] = src[v];
     }
   }
-  ds_rank_group<MODE>(GL, A.logits, T, E, K, A.idx, A.gates, blockIdx.x == 0, A.grp, A.status);
-  __syncthreads();
-  // Down-weight prefetch (few tokens): the routes' experts, read before the
-  // grouping scratch is overwritten.
-  int pf_e = -1;
-  if (A.pf.q != nullptr && lane < R) pf_e = GL.e[lane];
+  auto stage_x = [&]() {
+#pragma unroll
+    for (int u = 0; u < XCH; ++u) {
+      const int p = tid + NT * u;
+      if (p < T * nch) ds_store_chunk(xr[u], xs, xsum, p / nch, p % nch, nch);
+    }
+  };
+  // One token with ranked routes: its K routes go to K distinct experts, so
+  // the grouping is the ascending order of the chosen ids (sorted position of
+  // route f = chosen ids below its own). Every wave routes the token itself,
+  // which needs no LDS and no barrier before its first weight loads, and the
+  // x row is staged before any weight load is issued, so that waiting for it
+  // does not wait for those loads.
+  const bool one = MODE != kDsGiven && T == 1;
+  int pf_e = -1;  // route f's expert in lane f, for the down-weight prefetch
   int4 sl = make_int4(-1, 0, 0, 0);
-  {
+  uint64_t chosen = 0;          // one token: mask of the chosen ids
+  float gv = 0.0f;              // one token: lane f's gate
+  int id = -1, pos = 0, ex = -1;  // one token: lane f's id and sorted position; lane a's expert
+  if (one) {
+    if (MODE == TFM_ROUTE_OLMOE) {
+      uint16_t gb;
+      id = olmoe_route_wave<kF16>(A.logits, E, K, &gv, &gb, &chosen);
+    } else {
+      id = granite_route_wave<kF16>(A.logits, E, K, &gv, &chosen);
+    }
+    const bool route = lane < K;
+    pos = route ? __popcll(chosen & ((1ull << id) - 1ull)) : lane;
+    // Lane a < K receives the expert at sorted position a.
+    ex = __builtin_amdgcn_ds_permute(4 * pos, route ? id : -1);
+    sl = lane < K ? make_int4(ex, lane, lane + 1, K) : make_int4(-1, 0, 0, K);
+    if (A.pf.q != nullptr && route) pf_e = id;
+    stage_x();
+  } else {
+    ds_rank_group<MODE>(GL, A.logits, T, E, K, A.idx, A.gates, blockIdx.x == 0, A.grp, A.status);
+    __syncthreads();
+    // Down-weight prefetch (few tokens): the routes' experts, read before the
+    // grouping scratch is overwritten.
+    if (A.pf.q != nullptr && lane < R) pf_e = GL.e[lane];
     const int U = GL.act[E];
     if (lane < U) {
       const int ex = GL.act[lane];
@@ -502,42 +532,22 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     ds_load_row<C>(ds_mat(A.gate, e, N, H), n, H, ll, w.g);
     ds_load_row<C>(ds_mat(A.up, e, N, H), n, H, ll, w.u);
   };
-  DsGU<C> wA, wB;
-  if (wr.i0 < wr.i1) load(wA, wr.i0);
-  if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
-  for (int j = tid; j < R; j += NT) s_tok[j] = GL.order[j] / K;
-  __syncthreads();  // the grouping scratch is read; the x rows may overwrite it
-#pragma unroll
-  for (int u = 0; u < XCH; ++u) {
-    const int p = tid + NT * u;
-    if (p < T * nch) ds_store_chunk(xr[u], xs, xsum, p / nch, p % nch, nch);
-  }
-  __syncthreads();
 
-  auto emit = [&](int j, int n, float ag, float au) {
-    const float gt = dpp_group_sum<16>(ag);
-    const float up = dpp_group_sum<16>(au);
-    if (ll == 0 && n < N) {
-      const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
-      A.h[(int64_t)j * N + n] = f2st<kF16>(hv);
-    }
-  };
   // Down-weight prefetch. When the down projection runs as
   // ds_down_combine_kernel, its workgroup b' reads rows 4b'..4b'+3 of every
   // routed expert's down matrix: packed codes, scales and biases, three
   // contiguous runs. Workgroup b of this kernel copies them for b' = b,
   // b + grid, ... into a landing area that is never read. The XCDs' L2
   // caches are invalidated between kernels, but the copies stay in the
-  // Infinity Cache, which serves the down kernel's loads faster than HBM (at
-  // one token down+combine takes 7.6 instead of 8.9 us, this kernel 14.2
-  // instead of 13.0: the layer gains 0.35 us). A wave issues its share
-  // (routes w, w + NT/64, ...) after its first item's loads; the landing
-  // area is a separate object, so the dot products' LDS reads do not wait
-  // for these copies.
+  // Infinity Cache, which serves the down kernel's loads faster than HBM.
+  // Wave w copies routes w, w + NT/64, ... The compiler cannot tell the
+  // landing area from the staged x rows, so an LDS read issued after a copy
+  // waits for every load in flight: at one token the copies go out after the
+  // items (the weight stream bounds this kernel either way).
   __shared__ __attribute__((aligned(16))) uint4 s_sink[NT / 64][64];
   auto prefetch = [&]() {
     if (A.pf.q == nullptr) return;
-    const int nb = (A.H + 3) / 4, W = NT / 64, wave = tid >> 6;
+    const int nb = (A.H + 3) / 4, W = NT / 64, wave = uni(tid >> 6);
     const uint32_t qrow = (uint32_t)A.I * kBits / 8, srow = (uint32_t)A.I / 32;
     for (int bp = blockIdx.x; bp < nb; bp += gridDim.x) {
       for (int f = wave; f < R; f += W) {
@@ -553,6 +563,50 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     }
   };
 
+  DsGU<C> wA, wB;
+  if (one) {
+    if (wr.i0 < wr.i1) load(wA, wr.i0);
+    if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
+    asm volatile("; one-token barrier" ::: "memory");
+    __syncthreads();  // the x row is staged
+    // Published after the barrier: a barrier waits for the global stores in
+    // flight, and stores count in the same in-order counter as loads.
+    if (blockIdx.x == 0 && tid < 64) {
+      if (lane < K) {
+        A.idx[lane] = id;
+        A.gates[lane] = gv;
+        A.grp.order[pos] = lane;
+        A.grp.inverse[lane] = pos;
+        A.grp.gates_sorted[pos] = gv;
+        A.grp.active[lane] = ex;
+      }
+      if (lane < E) {
+        A.grp.offsets[lane] = __popcll(chosen & ((1ull << lane) - 1ull));
+        A.grp.slots[lane] = sl;
+      }
+      if (lane == 0) {
+        A.grp.offsets[E] = K;
+        A.grp.active[E] = K;
+      }
+    }
+  } else {
+    if (wr.i0 < wr.i1) load(wA, wr.i0);
+    if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
+    for (int j = tid; j < R; j += NT) s_tok[j] = GL.order[j] / K;
+    __syncthreads();  // the grouping scratch is read; the x rows may overwrite it
+    stage_x();
+    __syncthreads();
+    prefetch();
+  }
+
+  auto emit = [&](int j, int n, float ag, float au) {
+    const float gt = dpp_group_sum<16>(ag);
+    const float up = dpp_group_sum<16>(au);
+    if (ll == 0 && n < N) {
+      const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
+      A.h[(int64_t)j * N + n] = f2st<kF16>(hv);
+    }
+  };
   // Routes one at a time through one branch-free body (the nibble unpack is
   // redone per route: at decode most experts have one or two routes). PIPE
   // items are in flight per wave: when every route of item i is done, its
@@ -563,12 +617,11 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     const int j0 = uni(readlane_i(wr.sl.y, a)), j1 = uni(readlane_i(wr.sl.z, a));
     for (int j = j0; j < j1; ++j) {
       float ag, au;
-      ds_gu_dot<C>(w, xs, xsum, s_tok[j], ll, ag, au);
+      ds_gu_dot<C>(w, xs, xsum, one ? 0 : s_tok[j], ll, ag, au);
       emit(j, n, ag, au);
     }
     if (i + PIPE < wr.i1) load(w, i + PIPE);
   };
-  prefetch();
   if (PIPE == 1) {
     for (int i = wr.i0; i < wr.i1; ++i) step(wA, i);
   } else {
@@ -577,6 +630,7 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
       if (i + 1 < wr.i1) step(wB, i + 1);
     }
   }
+  if (one) prefetch();
 }
 
 // ---------------------------------------------------------------------------

@@ -10,9 +10,11 @@
 //    highest ranks fill slots rank-(E-K) in ascending order; gates are the fp32
 //    softmax over the K selected logits.
 //
-// Selection is K rounds of "largest remaining key": keys are the values mapped
-// to order-preserving unsigned integers, the maximum is a DPP wave reduction,
-// and a ballot of the lanes holding it resolves ties by id.
+// Selection is K rounds of "largest remaining key". A lane's key is unique: the
+// value's 16-bit storage pattern mapped to an order-preserving integer (NaN
+// placed by the rule), then the tie rule's id order in the low 6 bits; absent
+// and taken lanes hold 0. A round is one DPP maximum, and the winner's id is
+// the maximum's low bits.
 #pragma once
 
 #include "tfm_device.h"
@@ -70,6 +72,14 @@ __device__ __forceinline__ uint32_t sortable_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The same map for a non-NaN bf16 or half storage pattern: 16-bit keys whose
+// order is the values' order (-0 and +0 map alike). Both formats are sign and
+// magnitude, so equal keys mean equal values.
+__device__ __forceinline__ uint32_t sortable_key16(uint32_t u) {
+  u = u == 0x8000u ? 0u : u;
+  return (u & 0x8000u) ? (~u & 0xffffu) : (u | 0x8000u);
+}
+
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
   const uint32_t s = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
@@ -89,10 +99,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 
 // OLMoE routing of one token. row: E logits in the storage dtype (bf16, or
 // half when F16). Lane s < K of the wave returns slot s's expert id and gate
-// (others return -1 / 0); the gate's storage bits come back in *gate_bits.
+// (others return -1 / 0); the gate's storage bits come back in *gate_bits and,
+// when `selected` is given, the mask of the K chosen ids in *selected.
 template <bool F16 = false>
 __device__ __forceinline__ int olmoe_route_wave(const uint16_t* __restrict__ row, int E, int K,
-                                                float* gate, uint16_t* gate_bits) {
+                                                float* gate, uint16_t* gate_bits,
+                                                uint64_t* selected = nullptr) {
   const int lane = threadIdx.x & 63;
   const bool valid = lane < E;
   const float ld = valid ? st2f<F16>(row[lane]) : -__builtin_inff();
@@ -100,60 +112,53 @@ __device__ __forceinline__ int olmoe_route_wave(const uint16_t* __restrict__ row
   const float ex = wave_softmax_exp(ld, &norm);
   const uint16_t pb = f2st<F16>(ex * norm);
   const float p = st2f<F16>(pb);
-  // NaN ranks after every number: key 0, below sortable(-inf) = 0x007fffff.
-  uint32_t key = p != p ? 0u : sortable_key(p);
-  bool removed = !valid;
+  // Larger probabilities first, NaN after every number (key 1, below the key
+  // of -inf), equal values by increasing id (63 - id in the low bits). Every
+  // present lane's key is at least 64.
+  const uint32_t k16 = p != p ? 1u : sortable_key16(pb) + 2u;
+  uint32_t key = valid ? (k16 << 6) | (uint32_t)(63 - lane) : 0u;
   int my_idx = -1;
-  float my_gate = 0.0f;
-  uint16_t my_bits = 0;
   for (int slot = 0; slot < K; ++slot) {
-    const uint32_t kmax = wave_max_u32(removed ? 0u : key);
-    const uint64_t m = __ballot(!removed && key == kmax);
-    const int sel = __ffsll((unsigned long long)m) - 1;  // ties: lowest id
-    // Slot `slot` goes to lane `slot` of the result.
-    const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), sel));
-    const int gb = __builtin_amdgcn_readlane((int)pb, sel);
-    if (lane == slot) {
-      my_idx = sel;
-      my_gate = g;
-      my_bits = (uint16_t)gb;
-    }
-    if (lane == sel) removed = true;
+    const int sel = 63 - (int)(wave_max_u32(key) & 63u);
+    if (lane == slot) my_idx = sel;  // slot s goes to lane s of the result
+    if (lane == sel) key = 0u;
   }
-  *gate = my_gate;
-  *gate_bits = my_bits;
+  const int src = my_idx < 0 ? lane : my_idx;
+  const float g = __int_as_float(__shfl(__float_as_int(p), src, 64));
+  const int gb = __shfl((int)pb, src, 64);
+  *gate = my_idx < 0 ? 0.0f : g;
+  *gate_bits = my_idx < 0 ? (uint16_t)0 : (uint16_t)gb;
+  if (selected) *selected = __ballot(valid && key == 0u);
   return my_idx;
 }
 
 // Granite routing of one token. Lane s < K returns slot s's expert id and fp32
-// gate; other lanes return -1.
+// gate; other lanes return -1. With `selected`, *selected gets the mask of the
+// K chosen ids.
 template <bool F16 = false>
 __device__ __forceinline__ int granite_route_wave(const uint16_t* __restrict__ row, int E, int K,
-                                                  float* gate) {
+                                                  float* gate, uint64_t* selected = nullptr) {
   const int lane = threadIdx.x & 63;
   const bool valid = lane < E;
-  const float v = valid ? st2f<F16>(row[lane]) : 0.0f;
-  // NaN ranks above every number: key ~0u.
-  const uint32_t key = v != v ? 0xffffffffu : sortable_key(v);
-  bool removed = !valid;
+  const uint32_t vb = valid ? row[lane] : 0u;
+  const float v = st2f<F16>((uint16_t)vb);
+  // NaN ranks above every number (key 0x10001, above the key of +inf); equal
+  // values: the higher id ranks higher (id in the low bits). Every present
+  // lane's key is at least 64.
+  const uint32_t k16 = v != v ? 0x10001u : sortable_key16(vb) + 1u;
+  uint32_t key = valid ? (k16 << 6) | (uint32_t)lane : 0u;
   int my_idx = -1;
-  float my_val = 0.0f;
   for (int r = 0; r < K; ++r) {
-    const uint32_t kmax = wave_max_u32(removed ? 0u : key);
-    const uint64_t m = __ballot(!removed && key == kmax);
-    const int sel = 63 - __clzll((long long)m);  // ties: the higher id ranks higher
-    const int slot = K - 1 - r;
-    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), sel));
-    if (lane == slot) {
-      my_idx = sel;
-      my_val = sv;
-    }
-    if (lane == sel) removed = true;
+    const int sel = (int)(wave_max_u32(key) & 63u);
+    if (lane == K - 1 - r) my_idx = sel;
+    if (lane == sel) key = 0u;
   }
-  const float ld = lane < K ? my_val : -__builtin_inff();
+  const float sv = __int_as_float(__shfl(__float_as_int(v), my_idx < 0 ? lane : my_idx, 64));
+  const float ld = lane < K ? sv : -__builtin_inff();
   float norm;
   const float ex = wave_softmax_exp(ld, &norm);
   *gate = ex * norm;
+  if (selected) *selected = __ballot(valid && key == 0u);
   return my_idx;
 }
 
