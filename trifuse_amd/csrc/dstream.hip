@@ -806,6 +806,14 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
     fg = A.gates[lane];
     fpos = A.inverse[lane];
   }
+  // The residual of this lane's output row for both tokens, requested now so
+  // that the final sum does not wait for it.
+  float res[kDsSmallT] = {};
+  if (wave == 0 && ll == 0 && n < N && A.residual) {
+#pragma unroll
+    for (int t = 0; t < kDsSmallT; ++t)
+      if (t < T) res[t] = st2f<kF16>(A.residual[(int64_t)t * N + n]);
+  }
   // This wave's routes' weight rows, then every route's h row (sorted
   // position inverse[f]) into slot f. Bad routes' h rows were never written:
   // they are staged but not used.
@@ -838,16 +846,18 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
     if (ll == 0) s_p[f][rsub] = pr;
   }
   __syncthreads();
-  if (wave == 0 && ll == 0 && n < N) {
-    for (int t = 0; t < T; ++t) {
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < kDsSmallT; ++t) {
+      if (t >= T) break;
       float sacc = 0.0f;
       for (int k = 0; k < K; ++k) {
         const int f = t * K + k;
-        const int e = A.idx[f];
+        const int e = uni(readlane_i(fe, f));
         if (e >= 0 && e < E) sacc = __fadd_rn(sacc, s_p[f][rsub]);
       }
-      const float r = A.residual ? st2f<kF16>(A.residual[(int64_t)t * N + n]) : 0.0f;
-      A.y[(int64_t)t * N + n] = (uint16_t)pack_st2<kF16>(__builtin_fmaf(A.rmul, sacc, r), 0.0f);
+      if (ll == 0 && n < N)
+        A.y[(int64_t)t * N + n] = (uint16_t)pack_st2<kF16>(__builtin_fmaf(A.rmul, sacc, res[t]), 0.0f);
     }
   }
 }
