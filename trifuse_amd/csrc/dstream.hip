@@ -440,8 +440,12 @@ __device__ __forceinline__ void ds_gu_dot(const DsGU<C>& w, const uint4* __restr
   }
 }
 
-template <int C, int XCH, int NT, int PIPE, int MODE>
-__global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
+// CW = 1 adds one copy wave to the NT compute threads (workgroup NT + 64):
+// it routes like the others and then issues every down-weight copy of its
+// workgroup, so the compute waves' code holds no copy and their LDS reads
+// never wait for one.
+template <int C, int XCH, int NT, int PIPE, int MODE, int CW>
+__global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A) {
   extern __shared__ uint4 ds_lds[];
   const int H = A.H, N = A.I, T = A.T, K = A.K, E = A.E;
   const int R = T * K;
@@ -458,6 +462,9 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
   const int lane = tid & 63;
   const int ll = lane & 15, rsub = lane >> 4;
   const int gw = blockIdx.x * (NT / 64) + (tid >> 6), nw = gridDim.x * (NT / 64);
+  // The copy wave (CW = 1): its thread ids start at NT, past every x chunk
+  // (XCH = 1 and T * nch <= NT), the routes and the route tokens.
+  const bool copier = CW != 0 && (tid >> 6) == NT / 64;
 
   // Prologue. The x rows of every token (at most XCH 32-element chunks per
   // thread) are requested first; every workgroup then routes and groups the
@@ -522,9 +529,9 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
       sl.w = U;
     }
   }
-  WaveRange wr;
+  WaveRange wr{};
   const int ipe = (N + 3) / 4;
-  wave_range(sl, ipe, gw, nw, wr);
+  if (!copier) wave_range(sl, ipe, gw, nw, wr);
   auto load = [&](DsGU<C>& w, int i) {
     const int a = i / ipe;
     const int e = uni(readlane_i(wr.sl.x, a));
@@ -547,18 +554,20 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
   __shared__ __attribute__((aligned(16))) uint4 s_sink[NT / 64][64];
   auto prefetch = [&]() {
     if (A.pf.q == nullptr) return;
-    const int nb = (A.H + 3) / 4, W = NT / 64, wave = uni(tid >> 6);
+    const int nb = (A.H + 3) / 4, wave = uni(tid >> 6);
+    const int f0 = CW ? 0 : wave, fs = CW ? 1 : NT / 64;  // the copy wave takes every route
+    uint4* sink = s_sink[CW ? 0 : wave];
     const uint32_t qrow = (uint32_t)A.I * kBits / 8, srow = (uint32_t)A.I / 32;
     for (int bp = blockIdx.x; bp < nb; bp += gridDim.x) {
-      for (int f = wave; f < R; f += W) {
+      for (int f = f0; f < R; f += fs) {
         const int e = uni(readlane_i(pf_e, f));
         if (e < 0 || e >= E) continue;
         const DsMat m = ds_mat(A.pf, e, A.H, A.I);
         const uint32_t q0 = 4u * bp * qrow, s0 = 4u * bp * srow;
-        for (uint32_t o = 0; o < 4 * qrow; o += 1024) ds_lds_copy16(m.q, s_sink[wave], q0 + o + 16u * lane);
+        for (uint32_t o = 0; o < 4 * qrow; o += 1024) ds_lds_copy16(m.q, sink, q0 + o + 16u * lane);
         const uint32_t so = 16u * lane < 4 * srow ? s0 + 16u * lane : 0x80000000u;
-        ds_lds_copy16(m.s, s_sink[wave], so);
-        ds_lds_copy16(m.b, s_sink[wave], so);
+        ds_lds_copy16(m.s, sink, so);
+        ds_lds_copy16(m.b, sink, so);
       }
     }
   };
@@ -596,7 +605,7 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     __syncthreads();  // the grouping scratch is read; the x rows may overwrite it
     stage_x();
     __syncthreads();
-    prefetch();
+    if (!CW) prefetch();
   }
 
   auto emit = [&](int j, int n, float ag, float au) {
@@ -622,15 +631,22 @@ __global__ __launch_bounds__(NT) void ds_gateup_kernel(DsGateUpArgs A) {
     }
     if (i + PIPE < wr.i1) load(w, i + PIPE);
   };
-  if (PIPE == 1) {
-    for (int i = wr.i0; i < wr.i1; ++i) step(wA, i);
-  } else {
-    for (int i = wr.i0; i < wr.i1; i += 2) {
-      step(wA, i);
-      if (i + 1 < wr.i1) step(wB, i + 1);
+  // The copy wave's copies sit on a branch of their own that joins the
+  // compute waves' only at the end, so that no LDS read of theirs follows a
+  // copy in program order.
+  if (!copier) {
+    if (PIPE == 1) {
+      for (int i = wr.i0; i < wr.i1; ++i) step(wA, i);
+    } else {
+      for (int i = wr.i0; i < wr.i1; i += 2) {
+        step(wA, i);
+        if (i + 1 < wr.i1) step(wB, i + 1);
+      }
     }
+    if (!CW && one) prefetch();
+  } else {
+    prefetch();
   }
-  if (one) prefetch();
 }
 
 // ---------------------------------------------------------------------------
@@ -933,6 +949,16 @@ static unsigned ds_grid(Kern kern, int threads, size_t lds, int64_t max_items) {
   return (unsigned)std::max<int64_t>(1, std::min(cap, want));
 }
 
+// ds_grid for a gate/up kernel with a copy wave: 320 threads per workgroup,
+// of which 4 waves take items.
+template <typename Kern>
+static unsigned ds_grid_cw(Kern kern, size_t lds, int64_t max_items) {
+  const int per_cu = env_int("TFM_DS_WG_PER_CU", resident_per_cu(kern, 320, lds), 1, 16);
+  const int64_t cap = (int64_t)device_cus() * per_cu;
+  const int64_t want = (max_items + 3) / 4;
+  return (unsigned)std::max<int64_t>(1, std::min(cap, want));
+}
+
 // Raises a kernel's dynamic LDS limit (64 KiB by default) once per kernel.
 template <typename Kern>
 static void allow_lds(Kern kern, size_t lds) {
@@ -970,9 +996,17 @@ void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32
   const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
   const int per = T * (H / 32);
   const int xch = per <= nt ? 1 : per <= 2 * nt ? 2 : 4;
-#define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                              \
-  ds_gateup_kernel<CV, XV, NV, PV, MV><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV, MV>, NV, lds, items), \
-                                         NV, lds, s>>>(A);
+  // A copy wave issues the down-weight copies (TFM_DS_COPY_WAVE=0: the
+  // compute waves do, after their items at one token).
+  const bool copy_wave = A.pf.q != nullptr && env_int("TFM_DS_COPY_WAVE", 1, 0, 1) == 1;
+#define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                                    \
+  if (copy_wave && XV == 1 && NV == 256 && PV == 1) {                                                    \
+    ds_gateup_kernel<CV, 1, 256, 1, MV, 1><<<ds_grid_cw(ds_gateup_kernel<CV, 1, 256, 1, MV, 1>, lds, items), \
+                                             320, lds, s>>>(A);                                          \
+  } else {                                                                                               \
+    ds_gateup_kernel<CV, XV, NV, PV, MV, 0><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV, MV, 0>, NV, lds, items), \
+                                              NV, lds, s>>>(A);                                          \
+  }
 #define TFM_DS_GU_M(CV, XV, NV, PV)                                         \
   if (mode == TFM_ROUTE_OLMOE) { TFM_DS_GU_P(CV, XV, NV, PV, TFM_ROUTE_OLMOE) }     \
   else if (mode == TFM_ROUTE_GRANITE) { TFM_DS_GU_P(CV, XV, NV, PV, TFM_ROUTE_GRANITE) } \
