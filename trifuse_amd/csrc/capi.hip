@@ -260,8 +260,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     }
     if (decode_small((int)T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, g.bits, ws.h, idx, gates, ws.grp.inverse, (int)T, K, E, H, I, w->down, residual,
-                             g.residual_multiplier, y, s);
+      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(kDsGivenRoutes, (int)T), idx, gates,
+                             ws.grp.inverse, (int)T, K, E, H, I, w->down, residual, g.residual_multiplier, y, s);
       return;
     }
     const int max_active = (int)(R < E ? R : E);
@@ -620,7 +620,8 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
     const int max_active = (int)(R < E ? R : E);
     if (decode_small(T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, g.bits, ws.h, ws.idx, ws.gates, ws.grp.inverse, T, K, E, H, I, weights->down,
+      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(g.route, T), ws.idx, ws.gates, ws.grp.inverse,
+                             T, K, E, H, I, weights->down,
                              static_cast<const uint16_t*>(residual), g.residual_multiplier,
                              static_cast<uint16_t*>(y), s);
     } else {

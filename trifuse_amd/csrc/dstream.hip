@@ -501,6 +501,7 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
   uint64_t chosen = 0;          // one token: mask of the chosen ids
   float gv = 0.0f;              // one token: lane f's gate
   int id = -1, pos = 0, ex = -1;  // one token: lane f's id and sorted position; lane a's expert
+  int ordv = 0;                   // one token: lane a's route
   if (one) {
     if (MODE == TFM_ROUTE_OLMOE) {
       uint16_t gb;
@@ -510,8 +511,9 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     }
     const bool route = lane < K;
     pos = route ? __popcll(chosen & ((1ull << id) - 1ull)) : lane;
-    // Lane a < K receives the expert at sorted position a.
+    // Lane a < K receives the expert and the route at sorted position a.
     ex = __builtin_amdgcn_ds_permute(4 * pos, route ? id : -1);
+    ordv = __builtin_amdgcn_ds_permute(4 * pos, lane);
     sl = lane < K ? make_int4(ex, lane, lane + 1, K) : make_int4(-1, 0, 0, K);
     if (A.pf.q != nullptr && route) pf_e = id;
     stage_x();
@@ -627,7 +629,8 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     for (int j = j0; j < j1; ++j) {
       float ag, au;
       ds_gu_dot<C>(w, xs, xsum, one ? 0 : s_tok[j], ll, ag, au);
-      emit(j, n, ag, au);
+      // One token: h row = route (ds_h_route_order); else sorted position.
+      emit(one ? uni(readlane_i(ordv, j)) : j, n, ag, au);
     }
     if (i + PIPE < wr.i1) load(w, i + PIPE);
   };
@@ -692,8 +695,13 @@ __device__ __forceinline__ void ds_dn_dot(const DsDn<C, RG>& w, const uint4* __r
       for (int g = 0; g < RG; ++g) ds_word_dot(w.r[g][c], q, v[q], d[g], dh[g]);
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
-      const float sc = st2f<kF16>((uint16_t)w.r[g][c].s);
-      const float cc = __builtin_fmaf(-code_corr(), sc, st2f<kF16>((uint16_t)w.r[g][c].b));
+      // Opaque copies: keep the conversions here, at the dot products. Moved
+      // up to the loads, they make a wave wait for one row's scales before it
+      // issues the next row's loads.
+      uint32_t sr = w.r[g][c].s, br = w.r[g][c].b;
+      asm volatile("" : "+v"(sr), "+v"(br));
+      const float sc = st2f<kF16>((uint16_t)sr);
+      const float cc = __builtin_fmaf(-code_corr(), sc, st2f<kF16>((uint16_t)br));
       acc[g] += ds_chunk_value(sc, d[g], dh[g], cc * xsm);
     }
   }
@@ -788,7 +796,8 @@ __global__ __launch_bounds__(NT) void ds_down_kernel(DsDownArgs A) {
 // the rows' products for routes w, w+4, .. (streaming the rows' weights of
 // each routed expert), and wave 0 sums each token's K products in k order.
 struct DsDownCombineArgs {
-  const uint16_t* h;        // [R, I] sorted rows
+  const uint16_t* h;        // [R, I]: route order (h_route_order) or sorted rows
+  int h_route_order;
   const int32_t* idx;       // [R] flat route -> expert
   const float* gates;       // [R] flat route gates
   const int32_t* inverse;   // [R] flat route -> sorted position
@@ -822,13 +831,33 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
     fg = A.gates[lane];
     fpos = A.inverse[lane];
   }
+  // h rows in route order (one token) need no position: their chunks are
+  // requested right after the route ids (which the weight loads wait for), at
+  // most kDsDcHold per thread, and staged after the
+  // weight loads are issued.
+  constexpr int kDsDcHold = 2;
+  const bool hold = A.h_route_order && R * nch <= kDsDcHold * 256;
+  uint4 hr[kDsDcHold][4];
+  if (hold) {
+#pragma unroll
+    for (int u = 0; u < kDsDcHold; ++u) {
+      const int p = tid + 256 * u;
+      if (p < R * nch) {
+        const uint4* src = reinterpret_cast<const uint4*>(A.h + (int64_t)(p / nch) * kin + 32 * (p % nch));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) hr[u][v] = src[v];
+      }
+    }
+  }
   // The residual of this lane's output row for both tokens, requested now so
   // that the final sum does not wait for it.
-  float res[kDsSmallT] = {};
+  // Kept as storage bits until the sum: converted here, they would make the
+  // wave wait for every load issued so far.
+  uint32_t res[kDsSmallT] = {};
   if (wave == 0 && ll == 0 && n < N && A.residual) {
 #pragma unroll
     for (int t = 0; t < kDsSmallT; ++t)
-      if (t < T) res[t] = st2f<kF16>(A.residual[(int64_t)t * N + n]);
+      if (t < T) res[t] = A.residual[(int64_t)t * N + n];
   }
   // This wave's routes' weight rows, then every route's h row (sorted
   // position inverse[f]) into slot f. Bad routes' h rows were never written:
@@ -840,10 +869,18 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
     const int e = uni(readlane_i(fe, min(f, R - 1)));
     if (f < R && e >= 0 && e < E) ds_load_row<C>(ds_mat(A.down, e, N, kin), n, kin, ll, wt[u].r[0]);
   }
-  for (int p = tid; p < R * nch; p += 256) {
-    const int f = p / nch, k = p % nch;
-    const int pos = __shfl(fpos, f, 64);
-    ds_stage_chunk(A.h + (int64_t)pos * kin + 32 * k, xs, xsum, f, k, nch);
+  if (hold) {
+#pragma unroll
+    for (int u = 0; u < kDsDcHold; ++u) {
+      const int p = tid + 256 * u;
+      if (p < R * nch) ds_store_chunk(hr[u], xs, xsum, p / nch, p % nch, nch);
+    }
+  } else {
+    for (int p = tid; p < R * nch; p += 256) {
+      const int f = p / nch, k = p % nch;
+      const int pos = A.h_route_order ? f : __shfl(fpos, f, 64);
+      ds_stage_chunk(A.h + (int64_t)pos * kin + 32 * k, xs, xsum, f, k, nch);
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -866,14 +903,13 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
 #pragma unroll
     for (int t = 0; t < kDsSmallT; ++t) {
       if (t >= T) break;
+      // Bad routes hold a product of +0, and the sum (from +0) is never -0,
+      // so adding them changes no bit: the K reads go out together.
       float sacc = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        const int f = t * K + k;
-        const int e = uni(readlane_i(fe, f));
-        if (e >= 0 && e < E) sacc = __fadd_rn(sacc, s_p[f][rsub]);
-      }
+      for (int k = 0; k < K; ++k) sacc = __fadd_rn(sacc, s_p[t * K + k][rsub]);
       if (ll == 0 && n < N)
-        A.y[(int64_t)t * N + n] = (uint16_t)pack_st2<kF16>(__builtin_fmaf(A.rmul, sacc, res[t]), 0.0f);
+        A.y[(int64_t)t * N + n] =
+            (uint16_t)pack_st2<kF16>(__builtin_fmaf(A.rmul, sacc, st2f<kF16>((uint16_t)res[t])), 0.0f);
     }
   }
 }
@@ -1069,12 +1105,12 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
 // staged in LDS, and each route's data sits in one lane).
 bool decode_small(int T, int K) { return T >= 1 && T <= kDsSmallT && T * K <= kDsSmallR; }
 
-void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,
+void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t* idx, const float* gates,
                             const int32_t* inverse, int T, int K, int E, int H, int I, const tfm_affine& down,
                             const uint16_t* residual, float rmul, uint16_t* y, hipStream_t s) {
   if (!decode_small(T, K)) fail(TFM_E_INVALID, "decode down+combine: batch too large");
   DsDownCombineArgs A{};
-  A.h = hsorted; A.idx = idx; A.gates = gates; A.inverse = inverse;
+  A.h = h; A.h_route_order = h_route_order ? 1 : 0; A.idx = idx; A.gates = gates; A.inverse = inverse;
   A.T = T; A.K = K; A.E = E; A.H = H; A.I = I; A.down = down; A.residual = residual; A.rmul = rmul; A.y = y;
   const int R = T * K;
   const size_t lds = (size_t)R * (I / 32) * 68;

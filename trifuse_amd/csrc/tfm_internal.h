@@ -118,6 +118,9 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
 // One set per storage dtype and code width: ds_bf16 (dstream.hip), ds_f16
 // (dstream_f16.hip), ds_bf16_i8 (dstream_i8.hip), ds_f16_i8 (dstream_f16_i8.hip).
 constexpr int kDsGivenRoutes = 2;
+// Row order of the gate/up kernel's h output: route order (h row f = flat
+// route f) for one token with ranked routes, expert-sorted order otherwise.
+inline bool ds_h_route_order(int mode, int T) { return mode != kDsGivenRoutes && T == 1; }
 #define TFM_DS_DECLS                                                                                     \
   bool decode_stream_fits(int T, int K, int E, int H, int I);                                             \
   void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,  \
@@ -127,8 +130,8 @@ constexpr int kDsGivenRoutes = 2;
   void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const tfm_affine& down,      \
                       const Grouping& g, float* P, hipStream_t s);                                        \
   bool decode_small(int T, int K);                                                                        \
-  void launch_ds_down_combine(const uint16_t* hsorted, const int32_t* idx, const float* gates,            \
-                              const int32_t* inverse, int T, int K, int E, int H, int I,                  \
+  void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t* idx,                 \
+                              const float* gates, const int32_t* inverse, int T, int K, int E, int H, int I, \
                               const tfm_affine& down, const uint16_t* residual, float rmul, uint16_t* y, \
                               hipStream_t s);
 namespace ds_bf16 { TFM_DS_DECLS }
@@ -160,12 +163,13 @@ inline void launch_ds_down(bool f16, int bits, const uint16_t* hsorted, int H, i
                            const tfm_affine& down, const Grouping& g, float* P, hipStream_t s) {
   TFM_DS_PICK(f16, bits, launch_ds_down(hsorted, H, I, max_active, down, g, P, s));
 }
-inline void launch_ds_down_combine(bool f16, int bits, const uint16_t* hsorted, const int32_t* idx,
-                                   const float* gates, const int32_t* inverse, int T, int K, int E, int H,
-                                   int I, const tfm_affine& down, const uint16_t* residual, float rmul,
-                                   uint16_t* y, hipStream_t s) {
+inline void launch_ds_down_combine(bool f16, int bits, const uint16_t* h, bool h_route_order,
+                                   const int32_t* idx, const float* gates, const int32_t* inverse, int T,
+                                   int K, int E, int H, int I, const tfm_affine& down,
+                                   const uint16_t* residual, float rmul, uint16_t* y, hipStream_t s) {
   TFM_DS_PICK(f16, bits,
-              launch_ds_down_combine(hsorted, idx, gates, inverse, T, K, E, H, I, down, residual, rmul, y, s));
+              launch_ds_down_combine(h, h_route_order, idx, gates, inverse, T, K, E, H, I, down, residual, rmul,
+                                     y, s));
 }
 #undef TFM_DS_PICK
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
