@@ -626,11 +626,14 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     const int a = i / ipe;
     const int n = (i - a * ipe) * 4 + rsub;
     const int j0 = uni(readlane_i(wr.sl.y, a)), j1 = uni(readlane_i(wr.sl.z, a));
+    // One token: h row = route (ds_h_route_order), the route of slot a (one
+    // route per slot); else the sorted position. Read once per item: a read
+    // per route raised the kernel to 191 registers.
+    const int hr0 = one ? uni(readlane_i(ordv, a)) : j0;
     for (int j = j0; j < j1; ++j) {
       float ag, au;
       ds_gu_dot<C>(w, xs, xsum, one ? 0 : s_tok[j], ll, ag, au);
-      // One token: h row = route (ds_h_route_order); else sorted position.
-      emit(one ? uni(readlane_i(ordv, j)) : j, n, ag, au);
+      emit(hr0 + (j - j0), n, ag, au);
     }
     if (i + PIPE < wr.i1) load(w, i + PIPE);
   };
