@@ -813,12 +813,14 @@ struct DsDownCombineArgs {
 
 constexpr int kDsSmallR = 16;  // routes of the small-batch layer
 
-template <int C>
-__global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs A) {
+// NT threads: NT/64 waves share the routes (route f to wave f mod NT/64).
+template <int C, int NT>
+__global__ __launch_bounds__(NT) void ds_down_combine_kernel(DsDownCombineArgs A) {
   extern __shared__ uint4 ds_lds[];
   __shared__ float s_p[kDsSmallR][4];  // product of route f for row 4*blockIdx.x + r
   constexpr int nch = 16 * C;
-  constexpr int FW = kDsSmallR / 4;    // routes per wave
+  constexpr int NW = NT / 64;
+  constexpr int FW = (kDsSmallR + NW - 1) / NW;  // routes per wave
   const int T = A.T, K = A.K, E = A.E, N = A.H, kin = A.I;
   const int R = T * K;
   uint4* xs = ds_lds;                                        // [R][4][nch]
@@ -839,12 +841,12 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
   // most kDsDcHold per thread, and staged after the
   // weight loads are issued.
   constexpr int kDsDcHold = 2;
-  const bool hold = A.h_route_order && R * nch <= kDsDcHold * 256;
+  const bool hold = A.h_route_order && R * nch <= kDsDcHold * NT;
   uint4 hr[kDsDcHold][4];
   if (hold) {
 #pragma unroll
     for (int u = 0; u < kDsDcHold; ++u) {
-      const int p = tid + 256 * u;
+      const int p = tid + NT * u;
       if (p < R * nch) {
         const uint4* src = reinterpret_cast<const uint4*>(A.h + (int64_t)(p / nch) * kin + 32 * (p % nch));
 #pragma unroll
@@ -868,18 +870,18 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
   DsDn<C, 1> wt[FW];
 #pragma unroll
   for (int u = 0; u < FW; ++u) {
-    const int f = wave + 4 * u;
+    const int f = wave + NW * u;
     const int e = uni(readlane_i(fe, min(f, R - 1)));
     if (f < R && e >= 0 && e < E) ds_load_row<C>(ds_mat(A.down, e, N, kin), n, kin, ll, wt[u].r[0]);
   }
   if (hold) {
 #pragma unroll
     for (int u = 0; u < kDsDcHold; ++u) {
-      const int p = tid + 256 * u;
+      const int p = tid + NT * u;
       if (p < R * nch) ds_store_chunk(hr[u], xs, xsum, p / nch, p % nch, nch);
     }
   } else {
-    for (int p = tid; p < R * nch; p += 256) {
+    for (int p = tid; p < R * nch; p += NT) {
       const int f = p / nch, k = p % nch;
       const int pos = A.h_route_order ? f : __shfl(fpos, f, 64);
       ds_stage_chunk(A.h + (int64_t)pos * kin + 32 * k, xs, xsum, f, k, nch);
@@ -888,7 +890,7 @@ __global__ __launch_bounds__(256) void ds_down_combine_kernel(DsDownCombineArgs 
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < FW; ++u) {
-    const int f = wave + 4 * u;
+    const int f = wave + NW * u;
     if (f >= R) break;
     const int e = uni(readlane_i(fe, f));
     float pr = 0.0f;
@@ -1118,9 +1120,16 @@ void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t
   const int R = T * K;
   const size_t lds = (size_t)R * (I / 32) * 68;
   const unsigned grid = (unsigned)((H + 3) / 4);
-#define TFM_DS_DC(CV)                                \
-  allow_lds(ds_down_combine_kernel<CV>, lds);        \
-  ds_down_combine_kernel<CV><<<grid, 256, lds, s>>>(A);
+  // Eight waves (one route each at one token) unless TFM_DS_DC_THREADS=256.
+  const int nt = env_int("TFM_DS_DC_THREADS", 512, 256, 512) >= 512 ? 512 : 256;
+#define TFM_DS_DC(CV)                                     \
+  if (nt == 512) {                                        \
+    allow_lds(ds_down_combine_kernel<CV, 512>, lds);      \
+    ds_down_combine_kernel<CV, 512><<<grid, 512, lds, s>>>(A); \
+  } else {                                                \
+    allow_lds(ds_down_combine_kernel<CV, 256>, lds);      \
+    ds_down_combine_kernel<CV, 256><<<grid, 256, lds, s>>>(A); \
+  }
   switch (I / 512) {
     case 1: TFM_DS_DC(1) break;
     case 2: TFM_DS_DC(2) break;
