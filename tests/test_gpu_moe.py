@@ -83,6 +83,16 @@ def test_olmoe_decode_t8_x16(gpu):
         del layer
 
 
+@pytest.mark.parametrize("T", [16, 17, 24, 32, 33, 64])
+def test_olmoe_batch_sweep(gpu, T):
+    """Both sides of the decode-streaming (T <= 16), decode-GEMV (T <= 32) and
+    grouped-GEMM path switches, every token checked."""
+    w = wl.get_workload(f"olmoe_t{T}")
+    log(f"moe {w.name}")
+    layer = wl.workload_layers(w, gpu)[0]
+    _check_layer(w.geometry, _block(w.geometry), wl.workload_x(w), layer, None)
+
+
 @pytest.mark.parametrize("deterministic", [False, True])
 def test_olmoe_prefill_t512(gpu, deterministic):
     w = wl.WORKLOADS["olmoe_prefill_t512"]

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import dataclasses
 import hashlib
+import re
 from typing import Dict, List, Optional
 
 import numpy as np
@@ -101,6 +102,23 @@ WORKLOADS: Dict[str, Workload] = {
                                        description="OLMoE MoE block, prefill 512 tokens, f16 packs with "
                                                    "the affine 4-bit router"),
 }
+
+
+_SWEEP = re.compile(r"^(olmoe|granite)_t([1-9][0-9]*)$")
+
+
+def get_workload(name: str) -> Workload:
+    """A named workload, or a batch-size point ``olmoe_t<N>`` / ``granite_t<N>``:
+    N tokens of that geometry with uniform routing (the sweep across the
+    decode-streaming, decode-GEMV and grouped-GEMM paths)."""
+    if name in WORKLOADS:
+        return WORKLOADS[name]
+    m = _SWEEP.match(name)
+    if m is None:
+        raise KeyError(f"unknown workload {name!r}")
+    geom = OLMOE if m.group(1) == "olmoe" else GRANITE
+    T = int(m.group(2))
+    return Workload(name, geom, T, 1, description=f"{geom.name} MoE block, {T} tokens (batch-size sweep)")
 
 
 def _key(*parts) -> int:
@@ -280,6 +298,6 @@ def gemm_flops(geom: Geometry, routes: int, which: str) -> int:
 
 __all__ = [
     "Geometry", "Workload", "OLMOE", "GRANITE", "WORKLOADS", "LayerWeights", "make_layer",
-    "make_x", "workload_layers", "workload_x", "algorithmic_bytes", "algorithmic_flops",
+    "make_x", "get_workload", "workload_layers", "workload_x", "algorithmic_bytes", "algorithmic_flops",
     "gemm_flops", "hash_u32", "SEED", "GROUP", "TIMING_LAYERS",
 ]
