@@ -830,7 +830,8 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
       __syncthreads();
     }
   };
-  // Live row blocks (uniform over the workgroup), in steps of four.
+  // Live row blocks (uniform over the workgroup), in steps of four (with
+  // 64-row tiles: 1, 2 or 4).
   const int live = min(MB, ((rows_valid + 63) / 64) * 4);
   if constexpr (MB == 16) {
     if (live == 16)
@@ -847,7 +848,14 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
     else
       main_loop(std::integral_constant<int, 4>{});
   } else {
-    main_loop(std::integral_constant<int, 4>{});
+    // 64-row tiles (few routes per expert): one or two live blocks when the
+    // tile holds at most 16 or 32 rows, so that empty rows cost no MFMAs.
+    if (rows_valid <= 16)
+      main_loop(std::integral_constant<int, 1>{});
+    else if (rows_valid <= 32)
+      main_loop(std::integral_constant<int, 2>{});
+    else
+      main_loop(std::integral_constant<int, 4>{});
   }
 
   // ---- epilogue ----
