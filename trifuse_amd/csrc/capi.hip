@@ -172,6 +172,19 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // fit one 32-element chunk per lane.
 // The streaming decode kernels read 4-bit or 8-bit weights in bf16 or half
 // storage (an affine router is dequantised first).
+// Routes up to which batches past the streaming decode kernels run the
+// decode GEMV kernels rather than the grouped GEMM: OLMoE measured 80.2 and
+// 88.4 us per layer at 17 and 20 tokens on the GEMV kernels (86.6 and 89.0
+// on the GEMM), 96.7 and 115.1 at 24 and 32 (89.9 and 90.7 on the GEMM).
+// TFM_DECODE_GEMV_MAX_ROUTES overrides.
+static int decode_gemv_max_routes() {
+  static const int v = [] {
+    const char* s = std::getenv("TFM_DECODE_GEMV_MAX_ROUTES");
+    return s ? std::atoi(s) : 160;
+  }();
+  return v;
+}
+
 static bool fused_decode(const tfm_geometry& g, int64_t R) {
   return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
@@ -219,15 +232,18 @@ static void check_affine(const tfm_affine& a, const char* name) {
   need_align16(a.q, name);
 }
 
+// Routes up to which expert products run the GEMV kernels (gemv.hip) instead
+// of the grouped GEMM: past about 160 routes (OLMoE 20 tokens) the GEMM's
+// 64-row tiles are faster (Granite decode 32: 65.4 -> 51.6 us per layer).
 static int gemv_threshold() {
   static int v = [] {
     const char* s = std::getenv("TFM_GEMV_MAX_ROUTES");
-    if (!s) return 256;
+    if (!s) return 160;
     char* end = nullptr;
     const long n = std::strtol(s, &end, 10);
     if (!end || *end != 0 || n < 0 || n > (1 << 30)) {
       std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_GEMV_MAX_ROUTES=%s\n", s);
-      return 256;
+      return 160;
     }
     return (int)n;
   }();
@@ -247,7 +263,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const bool small = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
   // The standalone GEMV kernels (gemv.hip) are 4-bit bf16 only.
   const bool gemv = small && !f16 && g.bits == 4;
-  if (!grouped && small && decode_stream_fits((int)T, K, E, H, I)) {
+  // The streaming kernels at the sizes where tfm_moe_forward runs them.
+  if (!grouped && fused_decode(g, R) && decode_stream_fits((int)T, K, E, H, I)) {
     // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
     // shapes, so both entry points give bit-identical results.
     Grouping gd = ws.grp;
@@ -639,7 +656,8 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
                                    reinterpret_cast<int32_t*>(gates_out), R, s);
     return;
   }
-  if (fused_decode(g, R) && !f16 && g.bits == 4 && g.router == TFM_ROUTER_DENSE) {
+  if (fused_decode(g, R) && R <= decode_gemv_max_routes() && !f16 && g.bits == 4 &&
+      g.router == TFM_ROUTER_DENSE) {
     {
       StageScope st(TFM_STAGE_ROUTER, s);
       launch_decode_route(g.route, static_cast<const uint16_t*>(x),
