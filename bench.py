@@ -282,7 +282,19 @@ def dominant_roofline(r: Runner, stages):
     U = r.distinct_experts()
     H, I = g.hidden, g.intermediate
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
-    streaming = r.wl.bits == 4  # the streaming decode kernels (bf16 or f16 storage)
+    R = T * g.top_k
+    # The library's decode path choice: the streaming kernels (every storage
+    # dtype and code width) while the token rows fit their prologue, else the
+    # decode GEMV kernels (4-bit, bf16, dense router) up to 160 routes, else
+    # the grouped GEMM.
+    streaming = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
+                 H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
+    gemv = (not streaming and R <= 160 and r.wl.bits == 4 and r.wl.dtype == "bf16" and
+            r.wl.router == "dense")
+    # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
+    # weights-in-registers grouped GEMM, everything else the LDS-dequant one
+    wr = r.wl.bits == 4 and H <= 2048 and H % 128 == 0
+    gemm_label = "ggemm_wr_kernel<gateup>" if wr else "ggemm_kernel<gateup>"
     if is_decode(r.wl):
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
@@ -290,12 +302,9 @@ def dominant_roofline(r: Runner, stages):
         # routed experts' down Q/S/B from HBM into L2 for the fused
         # down+combine kernel: those bytes are moved by this kernel.
         dn_bytes_expert = H * I * r.wl.bits // 8 + 2 * (H * I // 64) * 2
-        prefetch = (sum(U) / len(U) * dn_bytes_expert) if (streaming and T <= 2 and T * g.top_k <= 16) else 0.0
+        prefetch = (sum(U) / len(U) * dn_bytes_expert) if (streaming and T <= 2 and R <= 16) else 0.0
         achieved = (per_launch + prefetch) / dur_s / 1e9
-        # Up to 16 OLMoE tokens (T * H / 32 <= 1024) on the streaming kernels,
-        # up to 32 on the decode GEMV kernels.
-        label = ("ds_gateup_kernel" if streaming and T * H // 32 <= 1024 else
-                 "decode_gateup_kernel" if streaming else "ggemm_kernel<gateup>")
+        label = "ds_gateup_kernel" if streaming else "decode_gateup_kernel" if gemv else gemm_label
         return {"kernel": label,
                 "bound": "hbm", "achieved": achieved,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
@@ -305,10 +314,7 @@ def dominant_roofline(r: Runner, stages):
                 "us_per_launch": st["us_per_launch"]}
     flops = wl.gemm_flops(g, T * g.top_k, "gateup")
     achieved = flops / dur_s / 1e12
-    # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
-    # weights-in-registers kernel, everything else the LDS-dequant one
-    wr = r.wl.bits == 4 and H <= 2048 and H % 128 == 0
-    return {"kernel": "ggemm_wr_kernel<gateup>" if wr else "ggemm_kernel<gateup>", "bound": "mfma",
+    return {"kernel": gemm_label, "bound": "mfma",
             "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
             "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}

@@ -921,8 +921,8 @@ static bool use_tall(int64_t n_routes, int E) {
 // least 384 routes, 64 when they average at most 48, else 128
 // (TFM_GGEMM_TILE=64/128/256 forces one). Every m-tile streams its expert's
 // weights again, so 64-row tiles pay only while few experts pass 64 routes:
-// with OLMoE's 64 experts they measured 12% faster from 33 to 384 tokens,
-// even at 512 and 9% slower at 768.
+// with OLMoE's 64 experts they measured 12% faster than 128-row tiles from
+// 33 to 384 tokens, level with them at 512 and 9% slower at 768.
 static int wr_tile_rows(int64_t n_routes, int E) {
   const int o = tile_override();
   if (o == 64 || o == 128 || o == 256) return o;
