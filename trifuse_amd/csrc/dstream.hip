@@ -1083,6 +1083,12 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
   A.gates_sorted = g.gates_sorted; A.P = P;
   const int nt = ds_down_lds(I, 1024) <= 160 * 1024 - 4096 ? ds_threads() : 256;
   const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
+  // Rows per item at 512- and 1024-wide h rows (TFM_DS_DOWN_RG = 1, 2 or 4
+  // overrides): items of 2-4 KB of packed rows measured fastest, so 8 rows
+  // (4-bit codes; 8-bit at 512 wide) or 4 rows (8-bit at 1024 wide). Granite
+  // decode (512 wide) at 8 tokens: 36.3 us per layer with 16 rows, 34.8 with
+  // 8; 8-bit OLMoE at 8 tokens: 85.4 with 8 rows, 84.0 with 4.
+  const int rg = env_int("TFM_DS_DOWN_RG", kBits == 8 && I >= 1024 ? 1 : 2, 1, 4);
   const size_t lds = ds_down_lds(I, nt);
   switch (I / 512) {
 #define TFM_DS_DN_P(CV, RV, NV, PV)                                                                      \
@@ -1094,8 +1100,24 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
 #define TFM_DS_DN(CV, RV) \
   if (nt == 1024) { TFM_DS_DN_N(CV, RV, 1024) } else if (nt == 512) { TFM_DS_DN_N(CV, RV, 512) } \
   else { TFM_DS_DN_N(CV, RV, 256) }
-    case 1: TFM_DS_DN(1, 4) break;
-    case 2: TFM_DS_DN(2, 2) break;
+    case 1:
+      if (rg == 1) {
+        TFM_DS_DN(1, 1)
+      } else if (rg >= 4) {
+        TFM_DS_DN(1, 4)
+      } else {
+        TFM_DS_DN(1, 2)
+      }
+      break;
+    case 2:
+      if (rg == 1) {
+        TFM_DS_DN(2, 1)
+      } else if (rg >= 4) {
+        TFM_DS_DN(2, 4)
+      } else {
+        TFM_DS_DN(2, 2)
+      }
+      break;
     case 3: TFM_DS_DN(3, 1) break;
     case 4: TFM_DS_DN(4, 1) break;
 #undef TFM_DS_DN
