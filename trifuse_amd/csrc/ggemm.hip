@@ -917,17 +917,45 @@ static bool use_tall(int64_t n_routes, int E) {
   return n_routes >= (int64_t)E * 384;
 }
 
-// Tile rows of the weights-in-registers kernel: 256 when experts average at
-// least 384 routes, 64 when they average at most 48, else 128
-// (TFM_GGEMM_TILE=64/128/256 forces one). Every m-tile streams its expert's
-// weights again, so 64-row tiles pay only while few experts pass 64 routes:
-// with OLMoE's 64 experts they measured 12% faster than 128-row tiles from
-// 33 to 384 tokens, level with them at 512 and 9% slower at 768.
-static int wr_tile_rows(int64_t n_routes, int E) {
+static int gg_device_cus() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    return n;
+  }();
+  return cus;
+}
+
+// Tile rows of the weights-in-registers kernel (TFM_GGEMM_TILE=64/128/256
+// forces one), from the average routes per expert a = n_routes / E and the
+// tile count, with every expert's routes taken as a:
+//  * 64 while a <= 56: every m-tile streams its expert's weights again, so
+//    64-row tiles pay only while few experts pass 64 routes (OLMoE 33-384
+//    tokens 12% faster than 128-row tiles, level at 512, 9% slower at 768;
+//    Granite 256 tokens, a = 51: 58.6 against 62.6 us per layer);
+//  * 256 from a = 208: a 256-row tile dequantises its weights once for twice
+//    the rows (OLMoE 1792 tokens, a = 224: 309 against 319 us; 2048 tokens:
+//    305 against 331; at a = 192, 1536 tokens, 128-row tiles win, 265
+//    against 277);
+//  * 256 below that when 256-row tiles fit one round of the compute units and
+//    128-row tiles do not (Granite, 4 gate/up column tiles: 768 tokens,
+//    a = 154, 84.4 against 98.6 us; at 512 tokens both fit, and 128-row tiles
+//    win, 70.7 against 73.1);
+//  * else 128.
+// col_tiles: 256-row weight tiles across the output (gate/up: gate and up
+// rows together).
+static int wr_tile_rows(int64_t n_routes, int E, int64_t col_tiles) {
   const int o = tile_override();
   if (o == 64 || o == 128 || o == 256) return o;
-  if (use_tall(n_routes, E)) return 256;
-  return n_routes <= (int64_t)E * 48 ? 64 : 128;
+  if (n_routes <= (int64_t)E * 56) return 64;
+  if (n_routes >= (int64_t)E * 208) return 256;
+  const int64_t m128 = (n_routes + (int64_t)E * 128 - 1) / ((int64_t)E * 128);
+  const int64_t m256 = (n_routes + (int64_t)E * 256 - 1) / ((int64_t)E * 256);
+  const int64_t cus = gg_device_cus();
+  if (E * m128 * col_tiles > cus && E * m256 * col_tiles <= cus) return 256;
+  return 128;
 }
 
 static unsigned grid_for(int64_t n_routes, int E, int BM, int NT) {
@@ -970,7 +998,7 @@ static void launch_tile(const GgArgs& a, int64_t n_routes, int E, hipStream_t s)
 #ifndef GG_NO_WR
   if constexpr (BITS == 4) {
     if (a.Kin <= kLdsScaleKin && a.Kin % BK2 == 0) {
-      switch (wr_tile_rows(n_routes, E)) {
+      switch (wr_tile_rows(n_routes, E, MODE == kGgGateUp ? (2 * (int64_t)a.N + 255) / 256 : ((int64_t)a.N + 255) / 256)) {
         case 256: launch_wr<256, MODE, F16>(a, n_routes, E, s); break;
         case 64: launch_wr<64, MODE, F16>(a, n_routes, E, s); break;
         default: launch_wr<128, MODE, F16>(a, n_routes, E, s); break;
