@@ -285,12 +285,12 @@ def dominant_roofline(r: Runner, stages):
     R = T * g.top_k
     # The library's decode path choice: the streaming kernels (every storage
     # dtype and code width) while the token rows fit their prologue, else the
-    # decode GEMV kernels (4-bit, bf16, dense router) up to 160 routes, else
+    # decode GEMV kernels (4-bit, bf16, dense router) up to 176 routes, else
     # the grouped GEMM.
     streaming = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
                  T * (H // 32) * 68 + R * 4 <= 65536 and  # staged x rows in LDS
                  H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
-    gemv = (not streaming and R <= 160 and r.wl.bits == 4 and r.wl.dtype == "bf16" and
+    gemv = (not streaming and R <= 176 and r.wl.bits == 4 and r.wl.dtype == "bf16" and
             r.wl.router == "dense")
     # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
     # weights-in-registers grouped GEMM, everything else the LDS-dequant one

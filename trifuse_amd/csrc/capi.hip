@@ -173,14 +173,15 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // The streaming decode kernels read 4-bit or 8-bit weights in bf16 or half
 // storage (an affine router is dequantised first).
 // Routes up to which batches past the streaming decode kernels run the
-// decode GEMV kernels rather than the grouped GEMM: OLMoE measured 80.2 and
-// 88.4 us per layer at 17 and 20 tokens on the GEMV kernels (86.6 and 89.0
-// on the GEMM), 96.7 and 115.1 at 24 and 32 (89.9 and 90.7 on the GEMM).
+// decode GEMV kernels rather than the grouped GEMM (64-row tiles): OLMoE
+// measured 81.2 and 86.3 us per layer at 20 and 22 tokens on the GEMV kernels
+// (96.4 and 87.7 on the GEMM), 88.7 and 90.9 at 23 and 24 (88.4 and 88.5 on
+// the GEMM); Granite 50.5 and 52.3 at 22 and 23 tokens (50.7 and 50.9).
 // TFM_DECODE_GEMV_MAX_ROUTES overrides.
 static int decode_gemv_max_routes() {
   static const int v = [] {
     const char* s = std::getenv("TFM_DECODE_GEMV_MAX_ROUTES");
-    return s ? std::atoi(s) : 160;
+    return s ? std::atoi(s) : 176;
   }();
   return v;
 }
