@@ -283,15 +283,16 @@ def dominant_roofline(r: Runner, stages):
     H, I = g.hidden, g.intermediate
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
     R = T * g.top_k
-    # The library's decode path choice: the streaming kernels (every storage
-    # dtype and code width) while the token rows fit their prologue, else the
-    # decode GEMV kernels (4-bit, bf16, dense router) up to 176 routes, else
-    # the grouped GEMM.
-    streaming = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
-                 T * (H // 32) * 68 + R * 4 <= 65536 and  # staged x rows in LDS
-                 H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
-    gemv = (not streaming and R <= 176 and r.wl.bits == 4 and r.wl.dtype == "bf16" and
-            r.wl.router == "dense")
+    # The library's decode path choice: the decode GEMV kernels (4-bit codes,
+    # bf16 storage) up to 176 routes from 4 tokens; the streaming kernels
+    # (every storage dtype and code width) at 1 to 3 tokens and for batches
+    # the GEMV kernels do not run, while the token rows fit their prologue;
+    # else the grouped GEMM.
+    gemv = R <= 176 and r.wl.bits == 4 and r.wl.dtype == "bf16"
+    fits = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
+            T * (H // 32) * 68 + R * 4 <= 65536 and  # staged x rows in LDS
+            H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
+    streaming = fits and (T <= 3 or not gemv)
     # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
     # weights-in-registers grouped GEMM, everything else the LDS-dequant one
     wr = r.wl.bits == 4 and H <= 2048 and H % 128 == 0
@@ -321,10 +322,11 @@ def dominant_roofline(r: Runner, stages):
             "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}
 
 
-def measured_traffic(workload: str):
+def measured_traffic(workload: str, kernel: str):
     """HBM bytes per launch of the dominant (gate/up) kernel from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summaries (the JSON blocks of
-    profiles/pmc_*.md), or None."""
+    profiles/pmc_*.md), or None: only a summary of the kernel the workload
+    runs today counts."""
     import glob
     import re
 
@@ -337,7 +339,7 @@ def measured_traffic(workload: str):
                 d = json.loads(block)
             except ValueError:
                 continue
-            if workload in d:
+            if workload in d and d[workload].get("kernel") == kernel:
                 return d[workload].get("traffic_bytes")
     return None
 
@@ -425,7 +427,7 @@ def compact(name, rep):
            "gateup_us": round(ru["us_per_launch"], 2), "gateup_frac": round(ru["frac"], 4)}
     if "down" in rep["stages_us"]:
         out["down_us"] = round(rep["stages_us"]["down"], 2)
-    traffic = measured_traffic(name)
+    traffic = measured_traffic(name, ru["kernel"])
     if traffic is not None:
         out["gateup_traffic"] = traffic  # HBM bytes per gate/up launch (rocprofv3 counters)
     return out
@@ -457,7 +459,7 @@ def main():
     head, report = measure(args.workload, dev, args, args.steps, args.warmup, args.deterministic)
     log(f"[bench] {args.workload}: {report['best_per_layer_us']:.2f} us/layer ({report['step_mode']})")
     roof = dict(report["roofline_gateup"])
-    roof["traffic"] = measured_traffic(args.workload)
+    roof["traffic"] = measured_traffic(args.workload, roof["kernel"])
 
     per = {args.workload: report}
     if not args.no_extra:

@@ -83,25 +83,25 @@ def test_olmoe_decode_t8_x16(gpu):
         del layer
 
 
-@pytest.mark.parametrize("T", [14, 15, 16, 17, 22, 23, 24, 32, 33, 64])
+@pytest.mark.parametrize("T", [3, 4, 14, 15, 22, 23, 24, 32, 33, 64])
 def test_olmoe_batch_sweep(gpu, T):
-    """Both sides of the streaming-decode (up to 14 tokens: the staged x rows
-    fit 64 KiB of LDS), decode-GEMV (up to 176 routes, 22 tokens) and
-    grouped-GEMM path switches, and the GEMM's 64-row tiles, every token
-    checked."""
+    """Both sides of the streaming-decode (up to 3 tokens), decode-GEMV (up to
+    176 routes, 22 tokens) and grouped-GEMM path switches, the last size whose
+    staged x rows would fit the streaming kernels (14 tokens) and the GEMM's
+    64-row tiles, every token checked."""
     w = wl.get_workload(f"olmoe_t{T}")
     log(f"moe {w.name}")
     layer = wl.workload_layers(w, gpu)[0]
     _check_layer(w.geometry, _block(w.geometry), wl.workload_x(w), layer, None)
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 19, 20, 22, 23])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 19, 20, 22, 23])
 def test_granite_batch_sweep(gpu, T):
     """Granite (hidden 1536, 40 experts), every token checked: the one- and
-    two-token streaming layers, the four-kernel streaming layer up to its last
-    size (19 tokens: the staged x rows take 3296 B of LDS per token, 64 KiB at
-    most), the decode GEMV (20 and 22 tokens, up to 176 routes) and the
-    grouped GEMM (23 tokens, 184 routes)."""
+    two-token streaming layers, the four-kernel streaming layer (3 tokens),
+    the decode GEMV from 4 tokens (19 and 20 tokens on either side of the
+    streaming kernels' LDS limit, 22 tokens at 176 routes) and the grouped
+    GEMM (23 tokens, 184 routes)."""
     w = wl.get_workload(f"granite_t{T}")
     log(f"moe {w.name}")
     layer = wl.workload_layers(w, gpu)[0]

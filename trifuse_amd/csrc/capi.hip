@@ -186,6 +186,26 @@ static int decode_gemv_max_routes() {
   return v;
 }
 
+// Tokens up to which the streaming decode kernels take a batch that the
+// decode GEMV kernels (bf16 storage, 4-bit codes) could also run; past it the
+// GEMV kernels do (TFM_DS_MAX_TOKENS overrides). Batches no GEMV kernel runs
+// (half storage, 8-bit codes, the affine router) stream whenever they fit.
+// Per layer, streaming against GEMV: OLMoE 1 token 16.8 against 22.4 us,
+// 2 tokens 30.6 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
+// layers) 56.0 against 53.0, 12 tokens 75.6 against 63.2; Granite 1 token
+// 12.6 against 18.0, 2 tokens 17.6 against 21.1, 3 tokens 23.9 against 23.9,
+// 8 tokens 34.9 against 32.5. The one- and two-token streaming layer is three
+// kernels (the down projection fused with the combine); 3 tokens stay on the
+// streaming kernels too (0.9 us slower for OLMoE, level for Granite), so that
+// the smallest batches give the same bits as the general streaming layer.
+static int ds_max_tokens() {
+  static const int v = [] {
+    const char* s = std::getenv("TFM_DS_MAX_TOKENS");
+    return s ? std::atoi(s) : 3;
+  }();
+  return v;
+}
+
 static bool fused_decode(const tfm_geometry& g, int64_t R) {
   return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
@@ -234,17 +254,19 @@ static void check_affine(const tfm_affine& a, const char* name) {
 }
 
 // Routes up to which expert products run the GEMV kernels (gemv.hip) instead
-// of the grouped GEMM: past about 160 routes (OLMoE 20 tokens) the GEMM's
+// of the grouped GEMM: past about 176 routes (OLMoE 22 tokens) the GEMM's
 // 64-row tiles are faster (Granite decode 32: 65.4 -> 51.6 us per layer).
+// The same switch as tfm_moe_forward's decode GEMV, so that the hook path
+// runs the kernels the forward path runs on the same routes.
 static int gemv_threshold() {
   static int v = [] {
     const char* s = std::getenv("TFM_GEMV_MAX_ROUTES");
-    if (!s) return 160;
+    if (!s) return 176;
     char* end = nullptr;
     const long n = std::strtol(s, &end, 10);
     if (!end || *end != 0 || n < 0 || n > (1 << 30)) {
       std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_GEMV_MAX_ROUTES=%s\n", s);
-      return 160;
+      return 176;
     }
     return (int)n;
   }();
@@ -265,7 +287,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   // The standalone GEMV kernels (gemv.hip) are 4-bit bf16 only.
   const bool gemv = small && !f16 && g.bits == 4;
   // The streaming kernels at the sizes where tfm_moe_forward runs them.
-  if (!grouped && fused_decode(g, R) && decode_stream_fits((int)T, K, E, H, I)) {
+  if (!grouped && fused_decode(g, R) && decode_stream_fits((int)T, K, E, H, I) &&
+      ((int)T <= ds_max_tokens() || !gemv)) {
     // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
     // shapes, so both entry points give bit-identical results.
     Grouping gd = ws.grp;
@@ -615,7 +638,8 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
   const int H = g.hidden_size, I = g.intermediate_size;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
-  if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I)) {
+  const bool gemv_decode = fused_decode(g, R) && R <= decode_gemv_max_routes() && !f16 && g.bits == 4;
+  if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I) && (T <= ds_max_tokens() || !gemv_decode)) {
     Grouping gd = ws.grp;
     gd.slots = ws.slots;
     gd.gates_sorted = ws.gates_sorted;
@@ -657,12 +681,15 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
                                    reinterpret_cast<int32_t*>(gates_out), R, s);
     return;
   }
-  if (fused_decode(g, R) && R <= decode_gemv_max_routes() && !f16 && g.bits == 4 &&
-      g.router == TFM_ROUTER_DENSE) {
+  if (gemv_decode) {
     {
       StageScope st(TFM_STAGE_ROUTER, s);
-      launch_decode_route(g.route, static_cast<const uint16_t*>(x),
-                          static_cast<const uint16_t*>(weights->router), weights->logit_bias, T,
+      const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
+      if (g.router == TFM_ROUTER_AFFINE) {
+        launch_dequant_router(false, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
+        rw = ws.router_w;
+      }
+      launch_decode_route(g.route, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
                           H, E, K, ws.logits, ws.idx, ws.gates, s);
     }
     // The gate/up kernel publishes the grouping with its slot table and
