@@ -188,8 +188,9 @@ static int decode_gemv_max_routes() {
 
 // Tokens up to which the streaming decode kernels take a batch that the
 // decode GEMV kernels (bf16 storage, 4-bit codes) could also run; past it the
-// GEMV kernels do (TFM_DS_MAX_TOKENS overrides). Batches no GEMV kernel runs
-// (half storage, 8-bit codes, the affine router) stream whenever they fit.
+// GEMV kernels do (TFM_DS_MAX_TOKENS overrides; an affine router is
+// dequantised first on either path). Batches no GEMV kernel runs (half
+// storage, 8-bit codes) stream whenever they fit.
 // Per layer, streaming against GEMV: OLMoE 1 token 16.8 against 22.4 us,
 // 2 tokens 30.6 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
 // layers) 56.0 against 53.0, 12 tokens 75.6 against 63.2; Granite 1 token
