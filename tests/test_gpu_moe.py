@@ -108,6 +108,18 @@ def test_granite_batch_sweep(gpu, T):
     _check_layer(w.geometry, _block(w.geometry), wl.workload_x(w), layer, None)
 
 
+@pytest.mark.parametrize("name", ["granite_t768", "olmoe_t1792"])
+def test_tall_tiles_below_384_routes(gpu, name):
+    """256-row grouped-GEMM tiles where experts average fewer than 384 routes:
+    Granite 768 tokens (154 per expert; 256-row tiles fit one round of the
+    compute units) and OLMoE 1792 tokens (224 per expert), every token
+    checked."""
+    w = wl.get_workload(name)
+    log(f"moe {w.name}")
+    layer = wl.workload_layers(w, gpu)[0]
+    _check_layer(w.geometry, _block(w.geometry), wl.workload_x(w), layer, None)
+
+
 @pytest.mark.parametrize("deterministic", [False, True])
 def test_olmoe_prefill_t512(gpu, deterministic):
     w = wl.WORKLOADS["olmoe_prefill_t512"]
