@@ -192,7 +192,7 @@ static int decode_gemv_max_routes() {
 // dequantised first on either path). Batches no GEMV kernel runs (half
 // storage, 8-bit codes) stream whenever they fit.
 // Per layer, streaming against GEMV: OLMoE 1 token 16.8 against 22.4 us,
-// 2 tokens 30.6 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
+// 2 tokens 26.4 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
 // layers) 56.0 against 53.0, 12 tokens 75.6 against 63.2; Granite 1 token
 // 12.6 against 18.0, 2 tokens 17.6 against 21.1, 3 tokens 23.9 against 23.9,
 // 8 tokens 34.9 against 32.5. The one- and two-token streaming layer is three
