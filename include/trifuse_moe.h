@@ -219,8 +219,9 @@ int tfm_moe_forward(const tfm_plan* plan, const void* x, int64_t tokens,
  * scratch memory is a static device array of TFM_STATIC_SCRATCH_BYTES inside
  * the library (one per GPU, held until the process ends) instead of a caller
  * workspace. Calls needing more scratch than that (tfm_workspace_bytes(plan,
- * tokens) > TFM_STATIC_SCRATCH_BYTES; OLMoE geometry: up to about 700 tokens)
- * fail with TFM_E_WORKSPACE. The call allocates nothing. Every call on a GPU
+ * tokens) > TFM_STATIC_SCRATCH_BYTES: past 776 tokens for OLMoE geometry
+ * with a dense router, 773 with an affine one; past 1105 tokens for Granite
+ * geometry, 1103 with an affine router) fail with TFM_E_WORKSPACE. The call allocates nothing. Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams,
  * other threads, other plans) race and must be ordered by the caller. Device
  * status bits (bad expert ids) of this variant are not reported. */
@@ -285,6 +286,15 @@ int tfm_profiler_attach(tfm_profiler* profiler); /* NULL detaches */
 int tfm_profiler_reset(tfm_profiler* profiler);
 int tfm_profiler_stage(tfm_profiler* profiler, int32_t stage, double* total_ms,
                        int32_t* launches, int32_t* dropped);
+/* Kernel-exact duration of a stage: the main kernel of each recorded stage
+ * launch (the first one it launches: the gate/up, down, combine, logits or
+ * fused routing kernel) is launched with hipExtLaunchKernelGGL events, which
+ * take the kernel dispatch's own start and end timestamps, the figures a
+ * rocprofv3 kernel trace reports, without the launch and cache-release gaps
+ * that the bracketing events of tfm_profiler_stage include. Returns the summed
+ * kernel durations (ms) and how many stage launches had such a kernel. */
+int tfm_profiler_stage_kernel(tfm_profiler* profiler, int32_t stage, double* kernel_ms,
+                              int32_t* kernels);
 const char* tfm_stage_name(int32_t stage);
 
 /* ---- diagnostics ----------------------------------------------------- */

@@ -45,10 +45,12 @@ def write_safetensors(path: Path, tensors: Dict[str, np.ndarray], metadata: Opti
 
 
 def write_checkpoint(out: Path, layers: List[dict], hidden: int, intermediate: int, top_k: int,
-                     bits: int = 4, bf16: bool = False) -> Dict[str, np.ndarray]:
+                     bits: int = 4, bf16: bool = False,
+                     metadata: Optional[dict] = None) -> Dict[str, np.ndarray]:
     """Per-expert checkpoint directory from `layers`: dicts of numpy arrays
     {gate,up,down}_{q (uint32), s, b (float16, or uint16 bf16 bits)} stacked
     [E, ...], and either router [E, H] or router_q/router_s/router_b.
+    `metadata` replaces the default {"format": "mlx"} header metadata.
     Returns the stacked tensors the loader must reproduce (name -> array)."""
     out = Path(out)
     out.mkdir(parents=True, exist_ok=False)
@@ -79,7 +81,7 @@ def write_checkpoint(out: Path, layers: List[dict], hidden: int, intermediate: i
                 halfs.add(name)
     norm = np.array([0.25, -2.0] + [1.0] * (hidden - 2), dtype=np.float16)
     tensors["model.norm.weight"] = stacked["model.norm.weight"] = norm
-    write_safetensors(out / "model.safetensors", tensors, {"format": "mlx"}, frozenset(halfs))
+    write_safetensors(out / "model.safetensors", tensors, metadata or {"format": "mlx"}, frozenset(halfs))
     config = {"model_type": "olmoe", "num_hidden_layers": len(layers), "num_experts": E,
               "hidden_size": hidden, "intermediate_size": intermediate, "num_experts_per_tok": top_k,
               "norm_topk_prob": False, "quantization": {"group_size": 64, "bits": bits}}

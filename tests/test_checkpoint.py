@@ -65,6 +65,31 @@ def test_write_stacked_round_trip(tmp_path):
         ck.write_stacked(d / "model.safetensors", out, cfg)
 
 
+def test_write_stacked_keeps_utf8_header(tmp_path):
+    """Non-ASCII metadata is written as UTF-8 with compact separators, as the
+    reference writer encodes its header (prepare_model.py:128), not as \\u escapes."""
+    rng = np.random.default_rng(5)
+    meta = {"format": "mlx", "note": "Grüße π 模型"}
+    d = tmp_path / "utf8"
+    write_checkpoint(d, [random_layer(rng, 2, 128, 128)], 128, 128, top_k=2, metadata=meta)
+    cfg = json.loads((d / "config.json").read_text())
+    out = tmp_path / "stacked_utf8.safetensors"
+    ck.write_stacked(d / "model.safetensors", out, cfg)
+    raw = out.read_bytes()
+    (n,) = struct.unpack("<Q", raw[:8])
+    head = raw[8:8 + n]
+    assert "Grüße π 模型".encode("utf8") in head
+    assert b"\\u" not in head
+    tensors, got, _ = ck.read_header(out)
+    assert got == meta
+    expect = {"__metadata__": meta}
+    expect.update({k: {"dtype": v["dtype"], "shape": v["shape"], "data_offsets": v["data_offsets"]}
+                   for k, v in tensors.items()})
+    enc = json.dumps(expect, separators=(",", ":"), ensure_ascii=False).encode("utf8")
+    enc += b" " * ((-len(enc)) % 8)
+    assert head == enc
+
+
 def test_layer_weights(tmp_path):
     d, lays, _ = _tiny(tmp_path)
     with ck.Checkpoint(d) as c:

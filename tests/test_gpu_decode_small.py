@@ -59,3 +59,27 @@ def test_small_batch_hook_matches_forward(gpu):
         y2 = blk.experts(x, idx, gates, wts)
         torch.cuda.synchronize()
         assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("route,K", [("olmoe", 32), ("olmoe", 17), ("granite", 24)])
+@pytest.mark.parametrize("T", [1, 2])
+def test_one_token_many_routes(gpu, route, K, T):
+    """More routes than the fused down + combine kernel takes (K > 16): one
+    token still ranks its routes in the gate/up prologue, but the separate
+    down kernel reads h in expert-sorted order, so the gate/up kernel must
+    write it that way. Against the oracle, and bit for bit against the
+    same tokens inside a three-token batch."""
+    geom = wl.Geometry(f"{route}_k{K}", 2048, 1024, 64, K, route)
+    log(f"decode one token many routes {route} K={K} T={T}")
+    layer = wl.make_layer(geom, 0, gpu, seed_tag=f"manyk{K}")
+    x = wl.make_x(geom, 3, tag=f"manyk_x{K}")
+    residual = wl.make_x(geom, 3, tag=f"manyk_r{K}")
+    blk = _block(geom)
+    _check_layer(geom, blk, x[:T].contiguous(), layer, np.arange(T, dtype=np.int32),
+                 residual=residual[:T].contiguous())
+    wts = tmoe.ExpertWeights.from_layer(layer)
+    xg, rg = x.to(gpu), residual.to(gpu)
+    y3 = blk.forward(xg, wts, residual=rg)
+    yT = blk.forward(xg[:T].contiguous(), wts, residual=rg[:T].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(yT, y3[:T])

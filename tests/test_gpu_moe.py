@@ -138,7 +138,7 @@ def test_olmoe_prefill_t4096_zipf(gpu):
     counts = np.bincount(ridx.reshape(-1), minlength=64)
     top4 = np.sort(counts)[::-1][:4].sum() / counts.sum()
     log(f"  top-4 expert share {top4:.3f}, hottest expert {counts.max()} routes")
-    assert 0.30 < top4 < 0.50
+    assert 0.36 <= top4 <= 0.44  # the skew the Zipf(1.1) rank profile is calibrated for
     # Every path reduces a token's K routes in k order: a second run, with or
     # without the deterministic flag and on a fresh block, is bit-identical.
     blk = _block(w.geometry)
@@ -261,6 +261,22 @@ def test_status_word_is_sticky(gpu):
         torch.cuda.synchronize()
         assert blk.status_word() & _lib.TFM_STATUS_BAD_EXPERT_ID, f"T={T}: bad id lost"
         assert blk.status_word() == 0        # read clears
+    # A bad small call, then a larger good call that needs a bigger workspace
+    # (the block swaps in a new one), then the read: the bit survives the swap.
+    blk = _block(geom)
+    x = wl.make_x(geom, 2, tag="sticky_swap").to(gpu)
+    _, idx, gates = blk.forward(x, wts, return_routes=True)
+    assert blk.status_word() == 0
+    small_ws = blk.workspace(2, gpu)
+    bad = idx.clone()
+    bad[0, 1] = -3
+    blk.experts(x, bad, gates, wts)
+    xl = wl.make_x(geom, 1024, tag="sticky_swap_big").to(gpu)
+    blk.forward(xl, wts)
+    assert blk.workspace(1024, gpu).data_ptr() != small_ws.data_ptr()
+    torch.cuda.synchronize()
+    assert blk.status_word() & _lib.TFM_STATUS_BAD_EXPERT_ID, "bad id lost in the workspace swap"
+    assert blk.status_word() == 0
 
 
 def test_host_mirror_rejects_bad_arguments(gpu):

@@ -139,4 +139,4 @@ def test_route_large_T(gpu):
     counts = np.bincount(ridx.reshape(-1), minlength=64)
     top4 = np.sort(counts)[::-1][:4].sum() / counts.sum()
     log(f"  zipf top-4 share {top4:.3f}")
-    assert 0.30 < top4 < 0.50
+    assert 0.36 <= top4 <= 0.44  # the skew the Zipf(1.1) rank profile is calibrated for

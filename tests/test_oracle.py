@@ -378,3 +378,22 @@ def test_cpu_block_matches_reference(route, bits):
     err = np.abs(f(y) - ref).max() / np.abs(ref).max()
     assert err < 1e-2, err
     assert used >= 1
+
+
+def test_zipf_workload_top4_share():
+    """The skewed-routing workload (prefill 4096, Zipf(1.1) rank bias on the
+    router logits) sends 36-44% of its routes to its four hottest experts, on
+    the first and the last of the 16 layers a timing step rotates through,
+    by the oracle's own routing."""
+    from tests._util import u16
+    from trifuse_amd import workload as wl
+
+    w = wl.WORKLOADS["olmoe_prefill_t4096_zipf"]
+    x = u16(wl.workload_x(w))
+    for layer in (0, wl.TIMING_LAYERS - 1):
+        lay = wl.make_layer(w.geometry, layer, "cpu", zipf=True, seed_tag=w.name)
+        logits = oracle.router_logits(x, u16(lay.router), lay.logit_bias.numpy())
+        idx, _ = oracle.route_olmoe(logits, w.geometry.top_k)
+        counts = np.bincount(idx.reshape(-1), minlength=w.geometry.experts)
+        top4 = np.sort(counts)[::-1][:4].sum() / counts.sum()
+        assert 0.36 <= top4 <= 0.44, (layer, top4)

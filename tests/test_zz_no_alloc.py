@@ -4,6 +4,8 @@ instead of a caller workspace, so outputs, expert ids and gates are
 bit-identical. Two calls in a row, the second with fewer tokens (the scratch
 keeps the first call's contents), on the decode and the prefill paths, and a
 call beyond the static array's size is refused."""
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -49,3 +51,17 @@ def test_static_refuses_oversized_call(gpu):
     x = wl.make_x(geom, T, tag="static_big").to(gpu)
     with pytest.raises(_lib.TfmError, match="static array"):
         blk.forward_static(x, wts)
+
+
+@pytest.mark.parametrize("geom_name,router,limit", [("olmoe", "dense", 776), ("olmoe", "affine", 773),
+                                                    ("granite", "dense", 1105), ("granite", "affine", 1103)])
+def test_static_token_limit_is_documented_one(gpu, geom_name, router, limit):
+    """The token limits include/trifuse_moe.h states are the largest T whose
+    workspace fits the static array."""
+    geom = wl.OLMOE if geom_name == "olmoe" else wl.GRANITE
+    dtype = torch.float16 if router == "affine" else torch.bfloat16
+    blk = tmoe.MoEBlock(geom.hidden, geom.intermediate, geom.experts, geom.top_k, route=geom.route,
+                        dtype=dtype, router=router)
+    assert blk.workspace_bytes(limit) <= _lib.TFM_STATIC_SCRATCH_BYTES < blk.workspace_bytes(limit + 1)
+    text = (Path(__file__).resolve().parents[1] / "include" / "trifuse_moe.h").read_text()
+    assert f"{limit} " in text.replace("\n", " ")

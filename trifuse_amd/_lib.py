@@ -130,6 +130,7 @@ SIGNATURES = {
     "tfm_profiler_reset": (c_int, [c_void_p]),
     "tfm_profiler_stage": (c_int, [c_void_p, c_int32, POINTER(c_double), POINTER(c_int32),
                                    POINTER(c_int32)]),
+    "tfm_profiler_stage_kernel": (c_int, [c_void_p, c_int32, POINTER(c_double), POINTER(c_int32)]),
     "tfm_stage_name": (c_char_p, [c_int32]),
     "tfm_status_word": (c_int, [c_void_p, c_void_p, POINTER(c_uint32)]),
     "tfm_last_error": (c_char_p, []),

@@ -281,7 +281,9 @@ def write_stacked(source: Union[str, Path], dest: Union[str, Path], config: dict
         e = plan[name]
         header[name] = {"dtype": e.dtype, "shape": e.shape, "data_offsets": [cur, cur + e.nbytes]}
         cur += e.nbytes
-    enc = json.dumps(header, separators=(",", ":")).encode()
+    # The reference writer's encoding (prepare_model.py:128): compact separators,
+    # non-ASCII text kept as UTF-8 rather than \u escapes.
+    enc = json.dumps(header, separators=(",", ":"), ensure_ascii=False).encode("utf8")
     enc += b" " * ((-len(enc)) % 8)
     with Path(source).open("rb") as src, dest.open("xb") as out:
         out.write(struct.pack("<Q", len(enc)))

@@ -32,6 +32,7 @@ struct tfm_profiler {
   int dropped = 0;
   std::vector<hipEvent_t> start, end;
   std::vector<int> stage;
+  std::vector<tfm::KernelTimer> kernel;  // per slot: the stage's main kernel, timed by its dispatch
 };
 
 namespace tfm {
@@ -50,9 +51,13 @@ static void* g_scratch_addr[kMaxDevices];
 
 static thread_local std::string g_last_error;
 static thread_local tfm_profiler* g_profiler = nullptr;
+static thread_local KernelTimer* g_kernel_timer = nullptr;
+
+KernelTimer* pending_kernel_timer() { return g_kernel_timer; }
 
 // Records the stage's start event on construction and its end event on
-// destruction when a profiler is attached to the calling thread.
+// destruction when a profiler is attached to the calling thread, and offers
+// the slot's kernel event pair to the first kernel the stage launches.
 struct StageScope {
   tfm_profiler* p;
   int slot = -1;
@@ -65,10 +70,14 @@ struct StageScope {
     }
     slot = p->used++;
     p->stage[slot] = stage_id;
+    p->kernel[slot].used = false;
+    g_kernel_timer = &p->kernel[slot];
     (void)hipEventRecord(p->start[slot], s);
   }
   ~StageScope() {
-    if (slot >= 0) (void)hipEventRecord(p->end[slot], s);
+    if (slot < 0) return;
+    (void)hipEventRecord(p->end[slot], s);
+    g_kernel_timer = nullptr;
   }
   StageScope(const StageScope&) = delete;
   StageScope& operator=(const StageScope&) = delete;
@@ -172,19 +181,8 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // fit one 32-element chunk per lane.
 // The streaming decode kernels read 4-bit or 8-bit weights in bf16 or half
 // storage (an affine router is dequantised first).
-// Routes up to which batches past the streaming decode kernels run the
-// decode GEMV kernels rather than the grouped GEMM (64-row tiles): OLMoE
-// measured 81.2 and 86.3 us per layer at 20 and 22 tokens on the GEMV kernels
-// (96.4 and 87.7 on the GEMM), 88.7 and 90.9 at 23 and 24 (88.4 and 88.5 on
-// the GEMM); Granite 50.5 and 52.3 at 22 and 23 tokens (50.7 and 50.9).
-// TFM_DECODE_GEMV_MAX_ROUTES overrides.
-static int decode_gemv_max_routes() {
-  static const int v = [] {
-    const char* s = std::getenv("TFM_DECODE_GEMV_MAX_ROUTES");
-    return s ? std::atoi(s) : 176;
-  }();
-  return v;
-}
+// Batches past the streaming decode kernels run the decode GEMV kernels
+// rather than the grouped GEMM (64-row tiles) up to gemv_threshold() routes.
 
 // Tokens up to which the streaming decode kernels take a batch that the
 // decode GEMV kernels (bf16 storage, 4-bit codes) could also run; past it the
@@ -202,7 +200,14 @@ static int decode_gemv_max_routes() {
 static int ds_max_tokens() {
   static const int v = [] {
     const char* s = std::getenv("TFM_DS_MAX_TOKENS");
-    return s ? std::atoi(s) : 3;
+    if (!s) return 3;
+    char* end = nullptr;
+    const long n = std::strtol(s, &end, 10);
+    if (!end || end == s || *end != 0 || n < 0 || n > 256) {
+      std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_DS_MAX_TOKENS=%s\n", s);
+      return 3;
+    }
+    return (int)n;
   }();
   return v;
 }
@@ -254,18 +259,23 @@ static void check_affine(const tfm_affine& a, const char* name) {
   need_align16(a.q, name);
 }
 
-// Routes up to which expert products run the GEMV kernels (gemv.hip) instead
-// of the grouped GEMM: past about 176 routes (OLMoE 22 tokens) the GEMM's
-// 64-row tiles are faster (Granite decode 32: 65.4 -> 51.6 us per layer).
-// The same switch as tfm_moe_forward's decode GEMV, so that the hook path
-// runs the kernels the forward path runs on the same routes.
+// Routes up to which expert products run the GEMV kernels (decode.hip,
+// gemv.hip) instead of the grouped GEMM, on every entry point: the forward
+// path's decode GEMV, the hook path and tfm_gather_qmm, so that all of them
+// run the same kernels on the same routes. Past about 176 routes (OLMoE 22
+// tokens) the GEMM's 64-row tiles are faster: OLMoE measured 81.2 and 86.3 us
+// per layer at 20 and 22 tokens on the GEMV kernels (96.4 and 87.7 on the
+// GEMM), 88.7 and 90.9 at 23 and 24 (88.4 and 88.5 on the GEMM); Granite 50.5
+// and 52.3 at 22 and 23 tokens (50.7 and 50.9); Granite decode 32 65.4 on the
+// GEMV kernels against 51.6. TFM_GEMV_MAX_ROUTES overrides (an integer in
+// [0, 2^30]; anything else is reported and ignored).
 static int gemv_threshold() {
   static int v = [] {
     const char* s = std::getenv("TFM_GEMV_MAX_ROUTES");
     if (!s) return 176;
     char* end = nullptr;
     const long n = std::strtol(s, &end, 10);
-    if (!end || *end != 0 || n < 0 || n > (1 << 30)) {
+    if (!end || end == s || *end != 0 || n < 0 || n > (1 << 30)) {
       std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_GEMV_MAX_ROUTES=%s\n", s);
       return 176;
     }
@@ -302,7 +312,7 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     }
     if (decode_small((int)T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(kDsGivenRoutes, (int)T), idx, gates,
+      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(kDsGivenRoutes, (int)T, K), idx, gates,
                              ws.grp.inverse, (int)T, K, E, H, I, w->down, residual, g.residual_multiplier, y, s);
       return;
     }
@@ -639,7 +649,7 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
   const int H = g.hidden_size, I = g.intermediate_size;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
-  const bool gemv_decode = fused_decode(g, R) && R <= decode_gemv_max_routes() && !f16 && g.bits == 4;
+  const bool gemv_decode = fused_decode(g, R) && R <= plan->gemv_max_routes && !f16 && g.bits == 4;
   if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I) && (T <= ds_max_tokens() || !gemv_decode)) {
     Grouping gd = ws.grp;
     gd.slots = ws.slots;
@@ -663,7 +673,7 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
     const int max_active = (int)(R < E ? R : E);
     if (decode_small(T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(g.route, T), ws.idx, ws.gates, ws.grp.inverse,
+      launch_ds_down_combine(f16, g.bits, ws.h, ds_h_route_order(g.route, T, K), ws.idx, ws.gates, ws.grp.inverse,
                              T, K, E, H, I, weights->down,
                              static_cast<const uint16_t*>(residual), g.residual_multiplier,
                              static_cast<uint16_t*>(y), s);
@@ -903,12 +913,15 @@ int tfm_profiler_create(int32_t capacity, tfm_profiler** out) {
     p->start.assign((size_t)capacity, nullptr);
     p->end.assign((size_t)capacity, nullptr);
     p->stage.assign((size_t)capacity, -1);
+    p->kernel.assign((size_t)capacity, KernelTimer{});
     for (int i = 0; i < capacity; ++i) {
-      hipError_t a = hipEventCreate(&p->start[i]);
-      hipError_t b = a == hipSuccess ? hipEventCreate(&p->end[i]) : a;
-      if (b != hipSuccess) {
+      hipError_t err = hipEventCreate(&p->start[i]);
+      if (err == hipSuccess) err = hipEventCreate(&p->end[i]);
+      if (err == hipSuccess) err = hipEventCreate(&p->kernel[i].start);
+      if (err == hipSuccess) err = hipEventCreate(&p->kernel[i].end);
+      if (err != hipSuccess) {
         tfm_profiler_destroy(p);
-        check_hip(b, "hipEventCreate");
+        check_hip(err, "hipEventCreate");
       }
     }
     *out = p;
@@ -922,11 +935,16 @@ void tfm_profiler_destroy(tfm_profiler* p) {
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : p->end)
     if (e) (void)hipEventDestroy(e);
+  for (const KernelTimer& k : p->kernel) {
+    if (k.start) (void)hipEventDestroy(k.start);
+    if (k.end) (void)hipEventDestroy(k.end);
+  }
   delete p;
 }
 
 int tfm_profiler_attach(tfm_profiler* p) {
   g_profiler = p;
+  g_kernel_timer = nullptr;
   return TFM_OK;
 }
 
@@ -956,6 +974,25 @@ int tfm_profiler_stage(tfm_profiler* p, int32_t stage, double* total_ms, int32_t
     if (total_ms) *total_ms = sum;
     if (launches) *launches = n;
     if (dropped) *dropped = p->dropped;
+  });
+}
+
+int tfm_profiler_stage_kernel(tfm_profiler* p, int32_t stage, double* kernel_ms, int32_t* kernels) {
+  return guarded([&] {
+    need_ptr(p, "profiler");
+    need(stage >= 0 && stage < TFM_STAGE_COUNT, "unknown stage");
+    double sum = 0.0;
+    int n = 0;
+    for (int i = 0; i < p->used; ++i) {
+      if (p->stage[i] != stage || !p->kernel[i].used) continue;
+      check_hip(hipEventSynchronize(p->kernel[i].end), "hipEventSynchronize");
+      float ms = 0.0f;
+      check_hip(hipEventElapsedTime(&ms, p->kernel[i].start, p->kernel[i].end), "hipEventElapsedTime");
+      sum += ms;
+      ++n;
+    }
+    if (kernel_ms) *kernel_ms = sum;
+    if (kernels) *kernels = n;
   });
 }
 

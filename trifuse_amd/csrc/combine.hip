@@ -87,9 +87,9 @@ void launch_combine_sorted(bool f16, const float* P, const int32_t* inverse, con
   const int64_t n = (int64_t)T * (H / 8);
   const unsigned blocks = (unsigned)((n + 255) / 256);
   if (f16)
-    combine_sorted_kernel<8, true><<<blocks, 256, 0, s>>>(P, inverse, n_valid, T, K, H, residual, rmul, y);
+    tfm_launch(combine_sorted_kernel<8, true>, blocks, 256, 0, s, P, inverse, n_valid, T, K, H, residual, rmul, y);
   else
-    combine_sorted_kernel<8, false><<<blocks, 256, 0, s>>>(P, inverse, n_valid, T, K, H, residual, rmul, y);
+    tfm_launch(combine_sorted_kernel<8, false>, blocks, 256, 0, s, P, inverse, n_valid, T, K, H, residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 
@@ -154,9 +154,9 @@ void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, co
   const int64_t n = (int64_t)T * (H / 8);
   const unsigned blocks = (unsigned)((n + 255) / 256);
   if (f16)
-    combine_rows_kernel<true><<<blocks, 256, 0, s>>>(Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
+    tfm_launch(combine_rows_kernel<true>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
   else
-    combine_rows_kernel<false><<<blocks, 256, 0, s>>>(Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
+    tfm_launch(combine_rows_kernel<false>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 

@@ -231,11 +231,11 @@ template <bool F16>
 static void decode_logits_dt(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
                              int E, uint16_t* logits, hipStream_t s) {
   switch (H) {
-    case 512: decode_logits_kernel<8, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1024: decode_logits_kernel<16, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 1536: decode_logits_kernel<24, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    case 2048: decode_logits_kernel<32, F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
-    default: decode_logits_generic<F16><<<E, 256, 0, s>>>(x, router, bias, T, H, E, logits); break;
+    case 512: tfm_launch(decode_logits_kernel<8, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
+    case 1024: tfm_launch(decode_logits_kernel<16, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
+    case 1536: tfm_launch(decode_logits_kernel<24, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
+    case 2048: tfm_launch(decode_logits_kernel<32, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
+    default: tfm_launch(decode_logits_generic<F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
   }
 }
 
@@ -275,11 +275,11 @@ void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* ga
   const int max_active = T * K < E ? T * K : E;
   const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active);
   switch (lg) {
-    case 4: decode_gateup_kernel<4><<<grid, 256, 0, s>>>(A); break;
-    case 8: decode_gateup_kernel<8><<<grid, 256, 0, s>>>(A); break;
-    case 16: decode_gateup_kernel<16><<<grid, 256, 0, s>>>(A); break;
-    case 32: decode_gateup_kernel<32><<<grid, 256, 0, s>>>(A); break;
-    default: decode_gateup_kernel<64><<<grid, 256, 0, s>>>(A); break;
+    case 4: tfm_launch(decode_gateup_kernel<4>, grid, 256, 0, s, A); break;
+    case 8: tfm_launch(decode_gateup_kernel<8>, grid, 256, 0, s, A); break;
+    case 16: tfm_launch(decode_gateup_kernel<16>, grid, 256, 0, s, A); break;
+    case 32: tfm_launch(decode_gateup_kernel<32>, grid, 256, 0, s, A); break;
+    default: tfm_launch(decode_gateup_kernel<64>, grid, 256, 0, s, A); break;
   }
   check_hip(hipGetLastError(), "decode gate/up launch");
 }

@@ -66,7 +66,6 @@ constexpr int kQW = kBits / 4;  // 16-byte loads per 32-element chunk
 __host__ __device__ constexpr float code_corr() { return (kBits == 4 ? 1.0f : 17.0f) * code_base(kF16); }
 
 constexpr int kDsCostUnpack = 2;  // item cost = kDsCostUnpack + routes of its expert
-constexpr int kDsSmallT = 2;      // tokens up to which the three-kernel layer is used
 constexpr int kDsDownXB = 4;      // h rows staged per wave in the down kernel
 
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
@@ -496,6 +495,7 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
   // x row is staged before any weight load is issued, so that waiting for it
   // does not wait for those loads.
   const bool one = MODE != kDsGiven && T == 1;
+  const bool hro = ds_h_route_order(MODE, T, K);  // h rows in route order
   int pf_e = -1;  // route f's expert in lane f, for the down-weight prefetch
   int4 sl = make_int4(-1, 0, 0, 0);
   uint64_t chosen = 0;          // one token: mask of the chosen ids
@@ -626,10 +626,11 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     const int a = i / ipe;
     const int n = (i - a * ipe) * 4 + rsub;
     const int j0 = uni(readlane_i(wr.sl.y, a)), j1 = uni(readlane_i(wr.sl.z, a));
-    // One token: h row = route (ds_h_route_order), the route of slot a (one
-    // route per slot); else the sorted position. Read once per item: a read
-    // per route raised the kernel to 191 registers.
-    const int hr0 = one ? uni(readlane_i(ordv, a)) : j0;
+    // One token whose down projection is the fused down + combine kernel:
+    // h row = route (ds_h_route_order), the route of slot a (one route per
+    // slot); else the sorted position, which the separate down kernel reads.
+    // Read once per item: a read per route raised the kernel to 191 registers.
+    const int hr0 = hro ? uni(readlane_i(ordv, a)) : j0;
     for (int j = j0; j < j1; ++j) {
       float ag, au;
       ds_gu_dot<C>(w, xs, xsum, one ? 0 : s_tok[j], ll, ag, au);
@@ -810,8 +811,6 @@ struct DsDownCombineArgs {
   float rmul;
   uint16_t* y;  // [T, H]
 };
-
-constexpr int kDsSmallR = 16;  // routes of the small-batch layer
 
 // NT threads: NT/64 waves share the routes (route f to wave f mod NT/64).
 template <int C, int NT>
@@ -1043,13 +1042,13 @@ void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32
   // OLMoE 1 token 16.75 us with the copy wave, 17.36 without; 2 tokens 30.8
   // with, 26.4 without; Granite 2 tokens 17.8 either way.
   const bool copy_wave = A.pf.q != nullptr && env_int("TFM_DS_COPY_WAVE", T == 1 ? 1 : 0, 0, 1) == 1;
-#define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                                    \
-  if (copy_wave && XV == 1 && NV == 256 && PV == 1) {                                                    \
-    ds_gateup_kernel<CV, 1, 256, 1, MV, 1><<<ds_grid_cw(ds_gateup_kernel<CV, 1, 256, 1, MV, 1>, lds, items), \
-                                             320, lds, s>>>(A);                                          \
-  } else {                                                                                               \
-    ds_gateup_kernel<CV, XV, NV, PV, MV, 0><<<ds_grid(ds_gateup_kernel<CV, XV, NV, PV, MV, 0>, NV, lds, items), \
-                                              NV, lds, s>>>(A);                                          \
+#define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                              \
+  if (copy_wave && XV == 1 && NV == 256 && PV == 1) {                                              \
+    tfm_launch(ds_gateup_kernel<CV, 1, 256, 1, MV, 1>,                                             \
+               ds_grid_cw(ds_gateup_kernel<CV, 1, 256, 1, MV, 1>, lds, items), 320, lds, s, A);    \
+  } else {                                                                                         \
+    tfm_launch(ds_gateup_kernel<CV, XV, NV, PV, MV, 0>,                                            \
+               ds_grid(ds_gateup_kernel<CV, XV, NV, PV, MV, 0>, NV, lds, items), NV, lds, s, A);   \
   }
 #define TFM_DS_GU_M(CV, XV, NV, PV)                                         \
   if (mode == TFM_ROUTE_OLMOE) { TFM_DS_GU_P(CV, XV, NV, PV, TFM_ROUTE_OLMOE) }     \
@@ -1096,8 +1095,9 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
   switch (I / 512) {
 #define TFM_DS_DN_P(CV, RV, NV, PV)                                                                      \
   allow_lds(ds_down_kernel<CV, RV, NV, PV>, lds);                                                        \
-  ds_down_kernel<CV, RV, NV, PV><<<ds_grid(ds_down_kernel<CV, RV, NV, PV>, NV, lds,                      \
-                                           (int64_t)max_active * ((H + 4 * RV - 1) / (4 * RV))), NV, lds, s>>>(A);
+  tfm_launch(ds_down_kernel<CV, RV, NV, PV>,                                                             \
+             ds_grid(ds_down_kernel<CV, RV, NV, PV>, NV, lds, (int64_t)max_active * ((H + 4 * RV - 1) / (4 * RV))), \
+             NV, lds, s, A);
 #define TFM_DS_DN_N(CV, RV, NV) \
   if (pipe == 2 && NV == 256) { TFM_DS_DN_P(CV, RV, 256, 2) } else { TFM_DS_DN_P(CV, RV, NV, 1) }
 #define TFM_DS_DN(CV, RV) \
@@ -1150,10 +1150,10 @@ void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t
 #define TFM_DS_DC(CV)                                     \
   if (nt == 512) {                                        \
     allow_lds(ds_down_combine_kernel<CV, 512>, lds);      \
-    ds_down_combine_kernel<CV, 512><<<grid, 512, lds, s>>>(A); \
+    tfm_launch(ds_down_combine_kernel<CV, 512>, grid, 512, lds, s, A); \
   } else {                                                \
     allow_lds(ds_down_combine_kernel<CV, 256>, lds);      \
-    ds_down_combine_kernel<CV, 256><<<grid, 256, lds, s>>>(A); \
+    tfm_launch(ds_down_combine_kernel<CV, 256>, grid, 256, lds, s, A); \
   }
   switch (I / 512) {
     case 1: TFM_DS_DC(1) break;

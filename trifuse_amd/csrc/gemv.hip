@@ -85,7 +85,7 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   {                                                                                         \
     const int ur = 4 * (64 / LGV), upe = (N + ur - 1) / ur;                                 \
     const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active); \
-    gemv_kernel<LGV, MODE><<<grid, 256, 0, s>>>(x, rm, g, wa, wb, N, Kin, gates, out);      \
+    tfm_launch(gemv_kernel<LGV, MODE>, grid, 256, 0, s, x, rm, g, wa, wb, N, Kin, gates, out);      \
   }
   if (nch <= 4) TFM_GEMV_LAUNCH(4)
   else if (nch <= 8) TFM_GEMV_LAUNCH(8)

@@ -972,11 +972,9 @@ static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) 
   using C = GgCfg<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS>;
   const int NT = (a.N + C::OUT_COLS - 1) / C::OUT_COLS;
   if (a.Kin <= kLdsScaleKin)
-    ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, true>
-        <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+    tfm_launch(ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, true>, grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s, a);
   else
-    ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, false>
-        <<<grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s>>>(a);
+    tfm_launch(ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, false>, grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s, a);
 }
 
 // 4-bit weights, inputs up to 2048 wide and a multiple of 128: weights in
@@ -990,7 +988,7 @@ static void launch_wr(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
   // 17); workgroups past their XCD's run exit at once.
   unsigned grid = grid_for(n_routes, E, BM, NT);
   if (BM == 256) grid = ((grid / 8 * 29 + 16) / 17 + 2) * 8;
-  ggemm_wr_kernel<BM, MODE, F16><<<grid, 512, 0, s>>>(a);
+  tfm_launch(ggemm_wr_kernel<BM, MODE, F16>, grid, 512, 0, s, a);
 }
 
 template <int MODE, int BITS, bool F16>

@@ -191,18 +191,18 @@ static void launch_router_topk_c(int route_kind, const uint16_t* x, const uint16
   const bool few = blocks < 512;  // under 2048 tokens: eight waves per workgroup
   if (route_kind == TFM_ROUTE_OLMOE) {
     if (few)
-      router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 8><<<blocks, 512, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                          hist, logits_out);
+      tfm_launch(router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 8>, blocks, 512, 0, s, x, w, bias, T, H, E, K, idx, gates_f32,
+                 hist, logits_out);
     else
-      router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 4><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                          hist, logits_out);
+      tfm_launch(router_topk_kernel<C, TFM_ROUTE_OLMOE, F16, 4>, blocks, 256, 0, s, x, w, bias, T, H, E, K, idx, gates_f32,
+                 hist, logits_out);
   } else {
     if (few)
-      router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 8><<<blocks, 512, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                            hist, logits_out);
+      tfm_launch(router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 8>, blocks, 512, 0, s, x, w, bias, T, H, E, K, idx, gates_f32,
+                 hist, logits_out);
     else
-      router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 4><<<blocks, 256, 0, s>>>(x, w, bias, T, H, E, K, idx, gates_f32,
-                                                                            hist, logits_out);
+      tfm_launch(router_topk_kernel<C, TFM_ROUTE_GRANITE, F16, 4>, blocks, 256, 0, s, x, w, bias, T, H, E, K, idx, gates_f32,
+                 hist, logits_out);
   }
 }
 
@@ -256,14 +256,14 @@ static void launch_router_c(const uint16_t* x, const uint16_t* w, const float* b
     // Few tokens: one wave per (token, expert), so the router rows stream in
     // parallel across the chip.
     const int waves = T * E;
-    router_logits_kernel<C, 1, F16><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, 1, logits);
+    tfm_launch(router_logits_kernel<C, 1, F16>, (waves + 3) / 4, 256, 0, s, x, w, bias, T, H, E, 1, logits);
   } else {
     // Many tokens: a wave keeps 4 token rows in registers and walks 16
     // experts, reading router rows from L2.
     constexpr int TW = 4;
     const int EPW = 16;
     const int waves = ((T + TW - 1) / TW) * ((E + EPW - 1) / EPW);
-    router_logits_kernel<C, TW, F16><<<(waves + 3) / 4, 256, 0, s>>>(x, w, bias, T, H, E, EPW, logits);
+    tfm_launch(router_logits_kernel<C, TW, F16>, (waves + 3) / 4, 256, 0, s, x, w, bias, T, H, E, EPW, logits);
   }
 }
 
@@ -422,9 +422,9 @@ static void topk_hist_dt(int route_kind, const uint16_t* logits, int T, int E, i
                          float* gates_f32, int32_t* hist, hipStream_t s) {
   const unsigned blocks = (unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock);
   if (route_kind == TFM_ROUTE_OLMOE)
-    topk_hist_kernel<TFM_ROUTE_OLMOE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+    tfm_launch(topk_hist_kernel<TFM_ROUTE_OLMOE, F16>, blocks, 256, 0, s, logits, T, E, K, idx, gates_f32, hist);
   else
-    topk_hist_kernel<TFM_ROUTE_GRANITE, F16><<<blocks, 256, 0, s>>>(logits, T, E, K, idx, gates_f32, hist);
+    tfm_launch(topk_hist_kernel<TFM_ROUTE_GRANITE, F16>, blocks, 256, 0, s, logits, T, E, K, idx, gates_f32, hist);
 }
 
 void launch_topk_hist(int route_kind, bool f16, const uint16_t* logits, int T, int E, int K, int32_t* idx,

@@ -1,11 +1,13 @@
 // Internal host-side declarations shared by the library's translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 #include <string>
+#include <utility>
 
 #include "../../include/trifuse_moe.h"
 
@@ -21,6 +23,28 @@ void check_hip(hipError_t err, const char* what);
 void set_last_error(const std::string& message);
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Kernel-exact stage timing. While a stage profiler is attached to the
+// calling thread, each stage scope offers one event pair; the first kernel the
+// stage launches through tfm_launch takes it with hipExtLaunchKernelGGL,
+// which binds the events to the kernel dispatch itself (its start and end
+// timestamps), so the pair measures the kernel alone.
+struct KernelTimer {
+  hipEvent_t start = nullptr, end = nullptr;
+  bool used = false;
+};
+KernelTimer* pending_kernel_timer();  // the current stage's offer, or null
+
+template <typename... P, typename... A>
+inline void tfm_launch(void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t s, A&&... args) {
+  KernelTimer* t = pending_kernel_timer();
+  if (t && !t->used) {
+    t->used = true;
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, t->start, t->end, 0u, std::forward<A>(args)...);
+  } else {
+    kernel<<<grid, block, lds, s>>>(std::forward<A>(args)...);
+  }
+}
 
 // Workspace carve-up: regions are 256-byte aligned, in declaration order.
 struct Carver {
@@ -118,9 +142,17 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
 // One set per storage dtype and code width: ds_bf16 (dstream.hip), ds_f16
 // (dstream_f16.hip), ds_bf16_i8 (dstream_i8.hip), ds_f16_i8 (dstream_f16_i8.hip).
 constexpr int kDsGivenRoutes = 2;
+// Small batches whose down projection runs fused with the combine
+// (decode_small): at most kDsSmallT tokens and kDsSmallR routes.
+constexpr int kDsSmallT = 2;
+constexpr int kDsSmallR = 16;
 // Row order of the gate/up kernel's h output: route order (h row f = flat
-// route f) for one token with ranked routes, expert-sorted order otherwise.
-inline bool ds_h_route_order(int mode, int T) { return mode != kDsGivenRoutes && T == 1; }
+// route f) for one token with ranked routes whose down projection is the
+// fused down + combine kernel (K <= kDsSmallR); expert-sorted order
+// otherwise, which the separate down kernel reads.
+__host__ __device__ inline bool ds_h_route_order(int mode, int T, int K) {
+  return mode != kDsGivenRoutes && T == 1 && K <= kDsSmallR;
+}
 #define TFM_DS_DECLS                                                                                     \
   bool decode_stream_fits(int T, int K, int E, int H, int I);                                             \
   void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32_t* idx, float* gates,  \

@@ -364,7 +364,13 @@ class MoEBlock:
     def workspace(self, tokens: int, device) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
         if self._ws is None or self._ws.numel() < need or self._ws.device != torch.device(device):
-            self._ws = _workspace(need, device)
+            fresh = _workspace(need, device)
+            if self._ws is not None and self._ws.device == fresh.device:
+                # The status bits are sticky until status_word() reads them:
+                # carry the old header (first 256 bytes) into the new workspace,
+                # in stream order after every call that used the old one.
+                fresh[:256].copy_(self._ws[:256])
+            self._ws = fresh
         return self._ws
 
     def status_word(self) -> int:
@@ -622,6 +628,15 @@ class StageProfiler:
              ctypes.byref(n), ctypes.byref(dropped))
         if dropped.value:
             raise RuntimeError(f"profiler capacity exceeded ({dropped.value} stage launches dropped)")
+        return ms.value, n.value
+
+    def stage_kernel(self, name: str) -> Tuple[float, int]:
+        """(total ms, kernels) of the main kernel of each launch of one stage,
+        timed by the kernel dispatch's own start and end (as a kernel trace
+        reports it), without the launch gaps that stage() includes."""
+        ms = ctypes.c_double()
+        n = ctypes.c_int32()
+        call("tfm_profiler_stage_kernel", self._h, self.STAGES.index(name), ctypes.byref(ms), ctypes.byref(n))
         return ms.value, n.value
 
     def close(self):

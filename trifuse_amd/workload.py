@@ -257,13 +257,19 @@ def make_x(geom: Geometry, tokens: int, tag: str = "x", dtype=torch.bfloat16) ->
     return normal_bf16((tokens, geom.hidden), 1.0, _key(geom.name, tag, tokens), dtype)
 
 
+def workload_layer(wl: Workload, layer: int, device="cpu") -> LayerWeights:
+    """Layer `layer` of a workload. The two Granite workloads share weights
+    (prefill then decode)."""
+    tag = "shared" if wl.geometry is GRANITE else wl.name
+    return make_layer(wl.geometry, layer, device, zipf=wl.zipf, seed_tag=tag, bits=wl.bits,
+                      dtype=wl.torch_dtype, affine_router=wl.router == "affine")
+
+
 def workload_layers(wl: Workload, device="cpu", layers: Optional[int] = None) -> List[LayerWeights]:
     """Independently seeded layers of a workload (default: the workload's own
-    layer count). The two Granite workloads share weights (prefill then decode)."""
-    tag = "shared" if wl.geometry is GRANITE else wl.name
+    layer count)."""
     n = wl.layers if layers is None else layers
-    return [make_layer(wl.geometry, l, device, zipf=wl.zipf, seed_tag=tag, bits=wl.bits,
-                       dtype=wl.torch_dtype, affine_router=wl.router == "affine") for l in range(n)]
+    return [workload_layer(wl, l, device) for l in range(n)]
 
 
 # Distinct layers a timing loop rotates through: 16 layers of either geometry
@@ -297,7 +303,7 @@ def gemm_flops(geom: Geometry, routes: int, which: str) -> int:
 
 
 __all__ = [
-    "Geometry", "Workload", "OLMOE", "GRANITE", "WORKLOADS", "LayerWeights", "make_layer",
+    "Geometry", "Workload", "OLMOE", "GRANITE", "WORKLOADS", "LayerWeights", "make_layer", "workload_layer",
     "make_x", "get_workload", "workload_layers", "workload_x", "algorithmic_bytes", "algorithmic_flops",
     "gemm_flops", "hash_u32", "SEED", "GROUP", "TIMING_LAYERS",
 ]
