@@ -27,7 +27,15 @@ bit for bit. --report PATH writes the full per-workload record as JSON.
 "cpu_baseline" is the oracle's MLX-semantics CPU block on the host cores over
 a bounded sample of the headline workload (cycling through its 16 distinct
 layers so the host's last-level cache does not hold the weights), with all
-cores and with one thread.
+cores and with one thread; every other workload the CPU block runs (bf16
+storage, dense router) carries its own bounded sample (`cpu_tok_per_s` with
+all cores, at least 3 whole layers from 2048 tokens; `cpu_tok_per_s_1thread`).
+
+Kernel durations (`us_per_launch`, `gateup_us`, `down_us`) are the kernels' own:
+the stage profiler launches each stage's main kernel with events bound to its
+dispatch, the timestamps a rocprofv3 kernel trace reports. The events around
+each launch, which add the launch and cache-release gap, are kept beside them
+(`us_per_launch_events`).
 """
 from __future__ import annotations
 
@@ -99,6 +107,11 @@ def pmc_summary(root: str):
                 sums[k][row["Counter_Name"]] += float(row["Counter_Value"])
     out = {k: {"dispatches": len(disp[k]), **{c: v / len(disp[k]) for c, v in sorted(sums[k].items())}}
            for k in sums}
+    # The kernel sources the counters were read from (measured_traffic keys a
+    # figure to its kernel's source file).
+    here = os.path.dirname(os.path.abspath(__file__))
+    out["source_sha16"] = {os.path.relpath(p, here): source_sha16(os.path.relpath(p, here))
+                           for p in sorted(glob.glob(os.path.join(here, "trifuse_amd", "csrc", "*.hip")))}
     print(json.dumps(out, indent=1), flush=True)
 
 
@@ -164,13 +177,22 @@ class Runner:
         for w in self.weights:
             self.y = self.block.forward(self.x, w, deterministic=self.deterministic)
 
+    def route_stats(self):
+        """Per layer, from the GPU's own routing: distinct experts routed and
+        the share of routes taken by the four busiest experts (cached)."""
+        if getattr(self, "_route_stats", None) is None:
+            U, top4 = [], []
+            for w in self.weights:
+                _, idx, _ = self.block.forward(self.x, w, return_routes=True)
+                counts = self.torch.bincount(idx.reshape(-1).long(), minlength=self.geom.experts)
+                U.append(int((counts > 0).sum()))
+                top4.append(float(counts.sort(descending=True).values[:4].sum()) / float(counts.sum()))
+            self._route_stats = (U, top4)
+        return self._route_stats
+
     def distinct_experts(self):
         """Distinct experts routed per layer, from the GPU's own routing."""
-        out = []
-        for w in self.weights:
-            _, idx, _ = self.block.forward(self.x, w, return_routes=True)
-            out.append(int(self.torch.unique(idx).numel()))
-        return out
+        return self.route_stats()[0]
 
     def time_steps(self, steps, warmup):
         torch = self.torch
@@ -234,6 +256,9 @@ class Runner:
             ms, n = prof.stage(s)
             if n:
                 out[s] = {"us_per_launch": ms * 1e3 / n, "launches": n}
+            kms, kn = prof.stage_kernel(s)
+            if n and kn:
+                out[s]["kernel_us_per_launch"] = kms * 1e3 / kn
         prof.close()
         return out
 
@@ -263,6 +288,8 @@ def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages, graph
         "mfma_TFLOPs": tflops, "mfma_frac": tflops / BF16_PEAK_TFLOPS,
         "bound": bound,
         "stages_us": {k: round(v["us_per_launch"], 3) for k, v in stages.items()},
+        "stages_kernel_us": {k: round(v["kernel_us_per_launch"], 3) for k, v in stages.items()
+                             if "kernel_us_per_launch" in v},
     }
     if graph is not None:
         gms, same = graph
@@ -278,7 +305,13 @@ def dominant_roofline(r: Runner, stages):
 
     g, T = r.geom, r.wl.tokens
     st = stages["gateup"]
-    dur_s = st["us_per_launch"] * 1e-6
+    # The kernel's own duration (dispatch timestamps, as a kernel trace
+    # reports it); the bracketing events add the launch and cache-release gap.
+    kus = st.get("kernel_us_per_launch", st["us_per_launch"])
+    dur_s = kus * 1e-6
+    timing = {"us_per_launch": kus, "us_per_launch_events": st["us_per_launch"],
+              "timing": "kernel dispatch timestamps (hipExtLaunchKernelGGL events)"
+              if "kernel_us_per_launch" in st else "events around the launch"}
     U = r.distinct_experts()
     H, I = g.hidden, g.intermediate
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
@@ -312,21 +345,34 @@ def dominant_roofline(r: Runner, stages):
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                 "traffic": None, "alg_bytes_per_launch": per_launch + prefetch,
                 "prefetch_bytes_per_launch": prefetch,
-                "frac_gateup_bytes_only": per_launch / dur_s / 1e9 / HBM_PEAK_GBS,
-                "us_per_launch": st["us_per_launch"]}
+                "frac_gateup_bytes_only": per_launch / dur_s / 1e9 / HBM_PEAK_GBS, **timing}
     flops = wl.gemm_flops(g, T * g.top_k, "gateup")
     achieved = flops / dur_s / 1e12
     return {"kernel": gemm_label, "bound": "mfma",
             "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
-            "traffic": None, "alg_flops_per_launch": flops, "us_per_launch": st["us_per_launch"]}
+            "traffic": None, "alg_flops_per_launch": flops, **timing}
+
+
+def source_sha16(rel: str):
+    """First 16 hex digits of the SHA-256 of a repository file, or None."""
+    import hashlib
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
+    try:
+        with open(path, "rb") as f:
+            return hashlib.sha256(f.read()).hexdigest()[:16]
+    except OSError:
+        return None
 
 
 def measured_traffic(workload: str, kernel: str):
     """HBM bytes per launch of the dominant (gate/up) kernel from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summaries (the JSON blocks of
-    profiles/pmc_*.md), or None: only a summary of the kernel the workload
-    runs today counts."""
+    profiles/pmc_*.md), or None. A summary counts only for the kernel the
+    workload runs today and only while the kernel's source file hashes as it
+    did when the counters were read (its "source" and "source_sha16" keys), so
+    that a changed kernel never inherits an old figure."""
     import glob
     import re
 
@@ -339,8 +385,12 @@ def measured_traffic(workload: str, kernel: str):
                 d = json.loads(block)
             except ValueError:
                 continue
-            if workload in d and d[workload].get("kernel") == kernel:
-                return d[workload].get("traffic_bytes")
+            e = d.get(workload)
+            if not isinstance(e, dict) or e.get("kernel") != kernel:
+                continue
+            src, sha = e.get("source"), e.get("source_sha16")
+            if src and sha and source_sha16(src) == sha:
+                return e.get("traffic_bytes")
     return None
 
 
@@ -402,6 +452,19 @@ def cpu_baseline(r: Runner, seconds: float, one_thread_seconds: float, min_layer
     return out
 
 
+def has_cpu_block(w) -> bool:
+    """The oracle's CPU block runs bf16 storage with the dense router."""
+    return w.dtype == "bf16" and w.router == "dense"
+
+
+def workload_cpu_baseline(r: Runner):
+    """A bounded CPU-block sample of one workload: all cores over at least 2 s
+    (at least 3 whole layers from 2048 tokens), then one thread over at least
+    1 s (one whole layer from 2048 tokens), cycling over 3 distinct layers."""
+    big = r.wl.tokens >= 2048
+    return cpu_baseline(r, 2.0, 1.0, min_layers=3 if big else 1, nlayers=3)
+
+
 def measure(name, dev, args, steps, warmup, deterministic):
     """Eager, stage and HIP-graph timings of one workload."""
     r = Runner(name, dev, deterministic)
@@ -417,19 +480,35 @@ def measure(name, dev, args, steps, warmup, deterministic):
     return r, rep
 
 
-def compact(name, rep):
-    """Short per-workload summary for the output line."""
+def layer_frac(rep):
+    """Roofline fraction of the whole layer at the reported (best) step time."""
     frac = rep["hbm_frac"] if rep["bound"] == "hbm" else rep["mfma_frac"]
-    frac *= rep["per_layer_us"] / rep["best_per_layer_us"]  # eager -> the reported (best) step time
+    return frac * rep["per_layer_us"] / rep["best_per_layer_us"]
+
+
+def compact(name, rep):
+    """Short per-workload summary for the output line: kernel durations are
+    the kernels' own (dispatch timestamps), as a kernel trace reports them."""
     ru = rep["roofline_gateup"]
     out = {"per_layer_us": round(rep["best_per_layer_us"], 2), "tok_per_s": round(rep["best_tok_per_s"]),
-           "bound": rep["bound"], "layer_frac": round(frac, 4),
+           "bound": rep["bound"], "layer_frac": round(layer_frac(rep), 4),
            "gateup_us": round(ru["us_per_launch"], 2), "gateup_frac": round(ru["frac"], 4)}
-    if "down" in rep["stages_us"]:
-        out["down_us"] = round(rep["stages_us"]["down"], 2)
+    st = rep.get("stages_kernel_us") or rep["stages_us"]
+    if "down" in st:
+        out["down_us"] = round(st["down"], 2)
     traffic = measured_traffic(name, ru["kernel"])
     if traffic is not None:
         out["gateup_traffic"] = traffic  # HBM bytes per gate/up launch (rocprofv3 counters)
+    if "zipf_top4_share" in rep:
+        out["zipf_top4_share"] = rep["zipf_top4_share"]
+    cb = rep.get("cpu_baseline")
+    if cb:
+        out["cpu_tok_per_s"] = round(cb["value"], 1)
+        out["cpu_threads"] = cb["cores"]
+        if "threads_1" in cb:
+            out["cpu_tok_per_s_1thread"] = round(cb["threads_1"]["value"], 2)
+    elif "cpu_baseline_skipped" in rep:
+        out["cpu_tok_per_s"] = None
     return out
 
 
@@ -460,6 +539,7 @@ def main():
     log(f"[bench] {args.workload}: {report['best_per_layer_us']:.2f} us/layer ({report['step_mode']})")
     roof = dict(report["roofline_gateup"])
     roof["traffic"] = measured_traffic(args.workload, roof["kernel"])
+    roof["layer_frac"] = round(layer_frac(report), 4)  # the whole layer at the reported step time
 
     per = {args.workload: report}
     if not args.no_extra:
@@ -473,8 +553,16 @@ def main():
             r, rep = measure(name, dev, args, steps, max(3, args.warmup // 2), args.deterministic)
             per[name] = rep
             log(f"[bench] {name}: {rep['best_per_layer_us']:.2f} us/layer")
-            if name == PREFILL_METRIC and not args.no_cpu:
-                rep["cpu_baseline"] = cpu_baseline(r, 0.0, 0.0, min_layers=3, nlayers=3)
+            if r.wl.zipf:
+                top4 = r.route_stats()[1]
+                rep["zipf_top4_share"] = {"min": round(min(top4), 4), "mean": round(sum(top4) / len(top4), 4),
+                                          "max": round(max(top4), 4), "layers": len(top4)}
+            if not args.no_cpu:
+                if has_cpu_block(r.wl):
+                    log(f"[bench] {name}: CPU block")
+                    rep["cpu_baseline"] = workload_cpu_baseline(r)
+                else:
+                    rep["cpu_baseline_skipped"] = "the oracle's CPU block runs bf16 storage with a dense router only"
             del r
             torch.cuda.empty_cache()
 
@@ -508,12 +596,10 @@ def main():
         "workloads": {n: compact(n, r) for n, r in per.items()
                       if n not in (args.workload, PREFILL_METRIC)},
     }
+    report["cpu_baseline"] = cpu
     mc = {args.workload: compact(args.workload, report)}
     if PREFILL_METRIC in per:
-        pre = per[PREFILL_METRIC]
-        mc[PREFILL_METRIC] = compact(PREFILL_METRIC, pre)
-        if "cpu_baseline" in pre:
-            mc[PREFILL_METRIC]["cpu_tok_per_s"] = round(pre["cpu_baseline"]["value"], 1)
+        mc[PREFILL_METRIC] = compact(PREFILL_METRIC, per[PREFILL_METRIC])
     line["metric_configs"] = mc
     if args.report:
         with open(args.report, "w") as f:

@@ -96,8 +96,11 @@ void launch_combine_sorted(bool f16, const float* P, const int32_t* inverse, con
 // 8 columns per thread; H % 8 == 0. Y rows are expert outputs in the storage
 // dtype (bf16, or half when F16; the
 // reference's per-route gather_qmm output, MLXNativeGraniteMoEPrefill.h:684),
-// weighted by the fp32 gate and summed in k order.
-template <bool F16>
+// weighted by the fp32 gate and summed in k order. For K <= KMAX every
+// route's row index and gate, then every row, are requested before the first
+// is used (bad routes read row 0 and are dropped by a select), as in
+// combine_sorted_kernel; larger K takes the plain loop.
+template <int KMAX, bool F16>
 __global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ inverse,
                                                            const int32_t* __restrict__ n_valid,
@@ -113,20 +116,39 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const uint16_t* __res
 #pragma unroll
   for (int v = 0; v < 8; ++v) s[v] = 0.0f;
   const int nv = *n_valid;
-  for (int k = 0; k < K; ++k) {
-    const int64_t f = (int64_t)t * K + k;
-    const int64_t row = inverse[f];
-    if (row >= nv) continue;
-    const float gw = gates[f];
-    const uint4 a = *reinterpret_cast<const uint4*>(Y + row * H + c);
-    s[0] = __builtin_fmaf(gw, lo_st<F16>(a.x), s[0]);
-    s[1] = __builtin_fmaf(gw, hi_st<F16>(a.x), s[1]);
-    s[2] = __builtin_fmaf(gw, lo_st<F16>(a.y), s[2]);
-    s[3] = __builtin_fmaf(gw, hi_st<F16>(a.y), s[3]);
-    s[4] = __builtin_fmaf(gw, lo_st<F16>(a.z), s[4]);
-    s[5] = __builtin_fmaf(gw, hi_st<F16>(a.z), s[5]);
-    s[6] = __builtin_fmaf(gw, lo_st<F16>(a.w), s[6]);
-    s[7] = __builtin_fmaf(gw, hi_st<F16>(a.w), s[7]);
+  auto add = [&](float gw, const uint4& a, bool on) {
+    s[0] = on ? __builtin_fmaf(gw, lo_st<F16>(a.x), s[0]) : s[0];
+    s[1] = on ? __builtin_fmaf(gw, hi_st<F16>(a.x), s[1]) : s[1];
+    s[2] = on ? __builtin_fmaf(gw, lo_st<F16>(a.y), s[2]) : s[2];
+    s[3] = on ? __builtin_fmaf(gw, hi_st<F16>(a.y), s[3]) : s[3];
+    s[4] = on ? __builtin_fmaf(gw, lo_st<F16>(a.z), s[4]) : s[4];
+    s[5] = on ? __builtin_fmaf(gw, hi_st<F16>(a.z), s[5]) : s[5];
+    s[6] = on ? __builtin_fmaf(gw, lo_st<F16>(a.w), s[6]) : s[6];
+    s[7] = on ? __builtin_fmaf(gw, hi_st<F16>(a.w), s[7]) : s[7];
+  };
+  if (K <= KMAX) {
+    int row[KMAX];
+    float gw[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      row[k] = k < K ? inverse[(int64_t)t * K + k] : nv;
+      gw[k] = k < K ? gates[(int64_t)t * K + k] : 0.0f;
+    }
+    uint4 a[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      const int64_t r = row[k] < nv ? row[k] : 0;
+      a[k] = *reinterpret_cast<const uint4*>(Y + r * H + c);
+    }
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) add(gw[k], a[k], row[k] < nv);
+  } else {
+    for (int k = 0; k < K; ++k) {
+      const int64_t f = (int64_t)t * K + k;
+      const int64_t row = inverse[f];
+      if (row >= nv) continue;
+      add(gates[f], *reinterpret_cast<const uint4*>(Y + row * H + c), true);
+    }
   }
   float r[8];
   if (residual) {
@@ -154,9 +176,9 @@ void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, co
   const int64_t n = (int64_t)T * (H / 8);
   const unsigned blocks = (unsigned)((n + 255) / 256);
   if (f16)
-    tfm_launch(combine_rows_kernel<true>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
+    tfm_launch(combine_rows_kernel<8, true>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
   else
-    tfm_launch(combine_rows_kernel<false>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
+    tfm_launch(combine_rows_kernel<8, false>, blocks, 256, 0, s, Y, inverse, n_valid, gates, T, K, H, residual, rmul, y);
   check_hip(hipGetLastError(), "combine launch");
 }
 

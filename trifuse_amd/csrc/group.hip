@@ -109,7 +109,9 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
         const_cast<int32_t*>(hist), (short)0, (int)((uint32_t)nblocks * B * 4), 0x00020000);
     int tot0 = 0, tot1 = 0, pre0 = 0, pre1 = 0;
     constexpr int kBatch = 32;
-    for (int r0 = 0; r0 < nsb; r0 += kBatch) {
+    // One superblock (bsum null): the totals are its own chunks' sums.
+    const int nsb_sums = bsum ? nsb : 0;
+    for (int r0 = 0; r0 < nsb_sums; r0 += kBatch) {
       int v0[kBatch], v1[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
@@ -134,13 +136,19 @@ __global__ __launch_bounds__(THREADS) void scatter_kernel(
       for (int k = 0; k < kSuperChunks; ++k) {
         const int c = sbi * kSuperChunks + k;
         const uint32_t row = (uint32_t)c * B * 4;
-        v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < b && lane < B) ? row + lane * 4 : 0x80000000u, 0, 0);
-        v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < b && 64 + lane < B) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
+        const int cend = bsum ? b : nblocks;  // one superblock: every chunk, for the totals
+        v0[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < cend && lane < B) ? row + lane * 4 : 0x80000000u, 0, 0);
+        v1[k] = __builtin_amdgcn_raw_buffer_load_b32(rh, (c < cend && 64 + lane < B) ? row + (64 + lane) * 4 : 0x80000000u, 0, 0);
       }
 #pragma unroll
       for (int k = 0; k < kSuperChunks; ++k) {
-        pre0 += v0[k];
-        pre1 += v1[k];
+        const bool before = sbi * kSuperChunks + k < b;
+        pre0 += before ? v0[k] : 0;
+        pre1 += before ? v1[k] : 0;
+        if (!bsum) {
+          tot0 += v0[k];
+          tot1 += v1[k];
+        }
       }
     }
     // Offsets: exclusive scan of the valid experts' totals.
@@ -224,14 +232,19 @@ void launch_group_scatter(const int32_t* ids, int64_t n, int E, int chunk, int32
   }
   const int nsb = (nb + kSuperChunks - 1) / kSuperChunks;
   // Superblock sums live after the chunk histograms (group_hist_rows rows).
-  int32_t* bsum = hist + (int64_t)(nb + 1) * (E + 1);
-  superblock_sums_kernel<<<nsb, 64, 0, s>>>(hist, nb, E, bsum);
-  check_hip(hipGetLastError(), "group superblock sums launch");
+  // With a single superblock the scatter kernel sums its chunks itself
+  // (bsum null), which saves a dependent launch for small batches.
+  int32_t* bsum = nullptr;
+  if (nsb > 1) {
+    bsum = hist + (int64_t)(nb + 1) * (E + 1);
+    superblock_sums_kernel<<<nsb, 64, 0, s>>>(hist, nb, E, bsum);
+    check_hip(hipGetLastError(), "group superblock sums launch");
+  }
   // One wave per workgroup for small chunks (the routing kernel's chunks).
   if (chunk <= 64)
-    scatter_kernel<64><<<nb, 64, 0, s>>>(ids, n, E, chunk, hist, bsum, nb, g, status);
+    tfm_launch(scatter_kernel<64>, nb, 64, 0, s, ids, n, E, chunk, hist, bsum, nb, g, status);
   else
-    scatter_kernel<kScatterThreads><<<nb, kScatterThreads, 0, s>>>(ids, n, E, chunk, hist, bsum, nb, g, status);
+    tfm_launch(scatter_kernel<kScatterThreads>, nb, kScatterThreads, 0, s, ids, n, E, chunk, hist, bsum, nb, g, status);
   check_hip(hipGetLastError(), "group scatter launch");
 }
 

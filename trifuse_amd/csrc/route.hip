@@ -258,11 +258,14 @@ static void launch_router_c(const uint16_t* x, const uint16_t* w, const float* b
     const int waves = T * E;
     tfm_launch(router_logits_kernel<C, 1, F16>, (waves + 3) / 4, 256, 0, s, x, w, bias, T, H, E, 1, logits);
   } else {
-    // Many tokens: a wave keeps 4 token rows in registers and walks 16
-    // experts, reading router rows from L2.
+    // Many tokens: a wave keeps 4 token rows in registers and walks EPW
+    // experts, reading router rows from L2: as few experts per wave as keep
+    // about 2048 waves (EPW 1 to 16, a power of two).
     constexpr int TW = 4;
-    const int EPW = 16;
-    const int waves = ((T + TW - 1) / TW) * ((E + EPW - 1) / EPW);
+    const int64_t tiles = (T + TW - 1) / TW;
+    int EPW = 1;
+    while (EPW < 16 && tiles * ((E + 2 * EPW - 1) / (2 * EPW)) >= 2048) EPW *= 2;
+    const int waves = (int)(tiles * ((E + EPW - 1) / EPW));
     tfm_launch(router_logits_kernel<C, TW, F16>, (waves + 3) / 4, 256, 0, s, x, w, bias, T, H, E, EPW, logits);
   }
 }
