@@ -771,11 +771,20 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
       launch_router_logits(f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, (int)tokens, H, E,
                            ws.logits, s);
   }
-  if (!fused_route) {
+  // At most 256 routes: top-k and grouping in one workgroup (the streaming
+  // decode kernels' routing and grouping), one kernel instead of three.
+  const bool small_group = !fused_route && R <= 256;
+  if (small_group) {
+    StageScope st(TFM_STAGE_TOPK, s);
+    Grouping gd = ws.grp;
+    gd.slots = ws.slots;
+    gd.gates_sorted = ws.gates_sorted;
+    launch_ds_route_group(f16, g.route, ws.logits, T, E, K, ws.idx, ws.gates, gd, &ws.hdr->status, s);
+  } else if (!fused_route) {
     StageScope st(TFM_STAGE_TOPK, s);
     launch_topk_hist(g.route, f16, ws.logits, T, E, K, ws.idx, ws.gates, ws.hist, s);
   }
-  {
+  if (!small_group) {
     StageScope st(TFM_STAGE_GROUP, s);
     launch_group_scatter(ws.idx, R, E, kTopkTokensPerBlock * K, ws.hist, ws.grp, &ws.hdr->status, s);
   }

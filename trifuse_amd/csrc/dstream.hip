@@ -260,6 +260,19 @@ __device__ __forceinline__ void ds_rank_group(DsGroupLds& L, const uint16_t* __r
   }
 }
 
+// Routing and grouping alone (the prefill path's top-k and grouping for at
+// most 256 routes): one workgroup of 16 waves, each ranking every 16th token,
+// then ds_rank_group's grouping, published. One kernel instead of the top-k
+// and scatter kernels of larger batches.
+template <int MODE>
+__global__ __launch_bounds__(1024) void ds_route_group_kernel(const uint16_t* __restrict__ logits, int T, int E,
+                                                              int K, int32_t* __restrict__ idx,
+                                                              float* __restrict__ gates, Grouping g,
+                                                              uint32_t* __restrict__ status) {
+  __shared__ DsGroupLds L;
+  ds_rank_group<MODE>(L, logits, T, E, K, idx, gates, true, g, status);
+}
+
 // ---------------------------------------------------------------------------
 // Raw loads of one chunk of one row: 16 packed bytes and its group's scale and
 // bias (bf16 in the low half).
@@ -1129,6 +1142,16 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
     default: fail(TFM_E_UNSUPPORTED, "decode down: intermediate width");
   }
   check_hip(hipGetLastError(), "decode down launch");
+}
+
+void launch_ds_route_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
+                           float* gates, const Grouping& g, uint32_t* status, hipStream_t s) {
+  if (T * K > 256 || E > 64 || T <= 0) fail(TFM_E_INVALID, "route+group: more than 256 routes or 64 experts");
+  if (route_kind == TFM_ROUTE_OLMOE)
+    tfm_launch(ds_route_group_kernel<TFM_ROUTE_OLMOE>, 1, 1024, 0, s, logits, T, E, K, idx, gates, g, status);
+  else
+    tfm_launch(ds_route_group_kernel<TFM_ROUTE_GRANITE>, 1, 1024, 0, s, logits, T, E, K, idx, gates, g, status);
+  check_hip(hipGetLastError(), "route+group launch");
 }
 
 // At most kDsSmallT tokens and kDsSmallR routes (every route's h row is

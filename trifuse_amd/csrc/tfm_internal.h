@@ -165,7 +165,9 @@ __host__ __device__ inline bool ds_h_route_order(int mode, int T, int K) {
   void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t* idx,                 \
                               const float* gates, const int32_t* inverse, int T, int K, int E, int H, int I, \
                               const tfm_affine& down, const uint16_t* residual, float rmul, uint16_t* y, \
-                              hipStream_t s);
+                              hipStream_t s);                                                             \
+  void launch_ds_route_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,   \
+                             float* gates, const Grouping& g, uint32_t* status, hipStream_t s);
 namespace ds_bf16 { TFM_DS_DECLS }
 namespace ds_f16 { TFM_DS_DECLS }
 namespace ds_bf16_i8 { TFM_DS_DECLS }
@@ -202,6 +204,18 @@ inline void launch_ds_down_combine(bool f16, int bits, const uint16_t* h, bool h
   TFM_DS_PICK(f16, bits,
               launch_ds_down_combine(h, h_route_order, idx, gates, inverse, T, K, E, H, I, down, residual, rmul,
                                      y, s));
+}
+// Top-k and the stable grouping of at most 256 routes (T * K <= 256, E <= 64)
+// in one workgroup, from logits [T, E] in the storage dtype: flat idx and fp32
+// gates, then order, inverse, offsets, active list, slot table and sorted
+// gates, and the status word, as the streaming gate/up kernel's prologue
+// publishes them.
+inline void launch_ds_route_group(bool f16, int route_kind, const uint16_t* logits, int T, int E, int K,
+                                  int32_t* idx, float* gates, const Grouping& g, uint32_t* status, hipStream_t s) {
+  if (f16)
+    ds_f16::launch_ds_route_group(route_kind, logits, T, E, K, idx, gates, g, status, s);
+  else
+    ds_bf16::launch_ds_route_group(route_kind, logits, T, E, K, idx, gates, g, status, s);
 }
 #undef TFM_DS_PICK
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
