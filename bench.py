@@ -83,6 +83,8 @@ def parse():
     p.add_argument("--pmc-summary", default=None, metavar="DIR",
                    help="only summarise the rocprofv3 counter CSVs under DIR (mean per dispatch of "
                         "every counter, per kernel) as JSON and exit")
+    p.add_argument("--linear-only", action="store_true",
+                   help="measure the dense affine linear shapes only and print them")
     p.add_argument("--pmc-copy", type=int, default=0, metavar="MIB",
                    help="only run 5 device-to-device copies of MIB MiB (a kernel of known traffic, to "
                         "calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -317,11 +319,11 @@ def dominant_roofline(r: Runner, stages):
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
     R = T * g.top_k
     # The library's decode path choice: the decode GEMV kernels (4-bit codes,
-    # bf16 storage) up to 176 routes from 4 tokens; the streaming kernels
-    # (every storage dtype and code width) at 1 to 3 tokens and for batches
-    # the GEMV kernels do not run, while the token rows fit their prologue;
-    # else the grouped GEMM.
-    gemv = R <= 176 and r.wl.bits == 4 and r.wl.dtype == "bf16"
+    # bf16 or half storage) up to 176 routes from 4 tokens; the streaming
+    # kernels (every storage dtype and code width) at 1 to 3 tokens and for
+    # batches the GEMV kernels do not run, while the token rows fit their
+    # prologue; else the grouped GEMM.
+    gemv = R <= 176 and r.wl.bits == 4
     fits = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
             T * (H // 32) * 68 + R * 4 <= 65536 and  # staged x rows in LDS
             H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
@@ -480,6 +482,67 @@ def measure(name, dev, args, steps, warmup, deterministic):
     return r, rep
 
 
+# Dense affine linear shapes (quantized_matmul behind NativeLinearWeight,
+# MLXNativeLinear.h:42-48): OLMoE's q/k/v/o projections and its router as a
+# 4-bit affine matrix, at one token and at 512.
+LINEAR_SHAPES = {"olmoe_qproj": (2048, 2048), "olmoe_router": (64, 2048)}
+LINEAR_TOKENS = (1, 512)
+
+
+def measure_dense_linear(dev, calls: int = 256):
+    """tfm_affine_qmm per call, replayed from a HIP graph of `calls` calls that
+    rotate over distinct weight matrices (at least 512 MB of them where the
+    matrix is large enough, so that the Infinity Cache does not serve the
+    weights; the router's 73 KB matrices total 19 MB and stay cached)."""
+    import torch
+    from trifuse_amd import moe as tmoe
+    from trifuse_amd import workload as wl
+
+    out = {}
+    for name, (N, K) in LINEAR_SHAPES.items():
+        wbytes = N * K // 2 + 2 * (N * (K // 64)) * 2
+        nsets = max(1, min(calls, -(-(512 << 20) // wbytes)))
+        q = wl.packed_nibbles((nsets, N, K // 8), 70 + N, dev)
+        s = wl.uniform_scales((nsets, N, K // 64), 71 + N, dev)
+        b = (s.float() * -8.0).to(torch.bfloat16)
+        for T in LINEAR_TOKENS:
+            x = wl.normal_bf16((T, K), 1.0, 72 + T).to(dev)
+            def run():
+                for i in range(calls):
+                    tmoe.native_affine_qmm(x, q[i % nsets], s[i % nsets], b[i % nsets], 64, 4)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                run()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run()
+            graph.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            t0.record()
+            for _ in range(reps):
+                graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) * 1e3 / (reps * calls)
+            del graph
+            nbytes = wbytes + T * K * 2 + T * N * 2
+            flops = 2.0 * T * N * K
+            out[f"{name}_t{T}"] = {"n_out": N, "k_in": K, "tokens": T, "us_per_call": round(us, 3),
+                                   "weight_sets": nsets, "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                   "mfma_frac": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                   "path": "GEMV" if T <= 176 else "grouped GEMM",
+                                   "timing": "HIP graph replay of consecutive calls"}
+            log(f"[bench] dense linear {name} T={T}: {us:.2f} us per call")
+        del q, s, b
+        torch.cuda.empty_cache()
+    return out
+
+
 def layer_frac(rep):
     """Roofline fraction of the whole layer at the reported (best) step time."""
     frac = rep["hbm_frac"] if rep["bound"] == "hbm" else rep["mfma_frac"]
@@ -534,6 +597,10 @@ def main():
     torch.cuda.set_device(dev)
     from trifuse_amd import workload as wl
 
+    if args.linear_only:
+        print(json.dumps({"dense_linear": measure_dense_linear(dev)}), flush=True)
+        return
+
     log(f"[bench] workload {args.workload}: building resident weights")
     head, report = measure(args.workload, dev, args, args.steps, args.warmup, args.deterministic)
     log(f"[bench] {args.workload}: {report['best_per_layer_us']:.2f} us/layer ({report['step_mode']})")
@@ -566,6 +633,11 @@ def main():
             del r
             torch.cuda.empty_cache()
 
+    linear = None
+    if not args.no_extra:
+        log("[bench] dense affine linear")
+        linear = measure_dense_linear(dev)
+
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline")
@@ -596,6 +668,8 @@ def main():
         "workloads": {n: compact(n, r) for n, r in per.items()
                       if n not in (args.workload, PREFILL_METRIC)},
     }
+    if linear is not None:
+        line["workloads"]["dense_linear"] = linear
     report["cpu_baseline"] = cpu
     mc = {args.workload: compact(args.workload, report)}
     if PREFILL_METRIC in per:

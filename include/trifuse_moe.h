@@ -192,6 +192,19 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
                    int32_t dtype, int32_t sorted, void* out,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- dense affine linear ---------------------------------------------- */
+/* mlx::core::quantized_matmul(x, W, scales, biases, transpose=true, group,
+ * bits, "affine") behind NativeLinearWeight::operator() (MLXNativeLinear.h:42-48;
+ * op native_affine_qmm, native_affine_ops.py:39-52), flattened to rows:
+ *   out[r, :] = x[r, :] . W^T      r in [0, rows)
+ *   x [rows, k_in] dtype, w one matrix (Q [n_out, k_in*bits/32], S, B
+ *   [n_out, k_in/group]), out [rows, n_out] dtype.
+ * The same kernels as tfm_gather_qmm with one expert, without the grouping
+ * pass and without a workspace. */
+int tfm_affine_qmm(const void* x, int64_t rows, const tfm_affine* w, int32_t n_out,
+                   int32_t k_in, int32_t group_size, int32_t bits, int32_t dtype, void* out,
+                   void* stream);
+
 /* ---- the MoE block --------------------------------------------------- */
 /* Expert part of the block given routes: NativeMoEExpertHook::execute's
  * contract (MLXMoEExpertHook.h:43-51) - result = residual +

@@ -59,8 +59,10 @@ def _check(geom, T, bits=4, dtype=F16, rm=1.0, tag="f16", layer_id=0, router_bit
     return blk, layer, x
 
 
-@pytest.mark.parametrize("geom_name,T", [("olmoe", 1), ("olmoe", 8), ("olmoe", 512),
-                                         ("granite", 5), ("granite", 300)])
+# 1-3 tokens: streaming kernels; 4 up to 176 routes (OLMoE 22 tokens):
+# decode GEMV kernels; beyond: grouped GEMM.
+@pytest.mark.parametrize("geom_name,T", [("olmoe", 1), ("olmoe", 4), ("olmoe", 8), ("olmoe", 22),
+                                         ("olmoe", 23), ("olmoe", 512), ("granite", 5), ("granite", 300)])
 def test_block_f16_affine_router(gpu, geom_name, T):
     geom = wl.OLMOE if geom_name == "olmoe" else wl.GRANITE
     log(f"moe f16 affine router {geom_name} T={T}")
@@ -152,9 +154,12 @@ def test_forward_rmsnorm_f16(gpu):
 
 
 def test_f16_decode_paths_agree(gpu):
-    # At decode shapes half blocks take the streaming kernels: the hook (given
-    # routes) matches the whole block bit for bit, and one or two tokens (the
-    # fused down + combine) match the same tokens inside a three-token batch.
+    # Half blocks take the streaming kernels up to three tokens and the decode
+    # GEMV kernels from four (as bf16 blocks do): the hook (given routes)
+    # matches the whole block bit for bit, one or two tokens (the fused
+    # down + combine) match the same tokens inside a three-token batch, and the
+    # three-token batch matches the same tokens of an eight-token batch (the
+    # other kernel family) within the block tolerance.
     geom = wl.OLMOE
     log("f16 decode hook / small-batch agreement")
     gpu_dev = torch.device("cuda:0")
@@ -171,7 +176,9 @@ def test_f16_decode_paths_agree(gpu):
     torch.cuda.synchronize()
     assert torch.equal(y8, y8h)
     assert torch.equal(y2, y3[:2]) and torch.equal(y1, y3[:1])
-    assert torch.equal(y3, y8[:3])
+    a = oracle.st_to_f32(u16(y3), "f16").astype(np.float64)
+    b = oracle.st_to_f32(u16(y8[:3]), "f16").astype(np.float64)
+    assert max_rel(a, b) <= BLOCK_TOL
 
 
 @pytest.mark.parametrize("T", [4, 300])

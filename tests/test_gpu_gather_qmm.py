@@ -74,6 +74,52 @@ def test_native_affine_qmm(gpu):
     assert max_rel(oracle.bf16_to_f32(u16(out)).reshape(18, N), ref) <= BLOCK_TOL
 
 
+# OLMoE q/k/v/o projections (2048 x 2048), its router (64 x 2048) and the
+# Granite k/v projection (512 x 1536) at decode and prefill row counts, across
+# the GEMV/GEMM switch (176 rows).
+@pytest.mark.parametrize("N,Kin", [(2048, 2048), (64, 2048), (512, 1536)])
+@pytest.mark.parametrize("rows", [1, 8, 176, 177, 512])
+def test_native_affine_qmm_dense_shapes(gpu, N, Kin, rows):
+    """tfm_affine_qmm (no grouping pass) against the oracle's fp64 product and
+    bit for bit against the grouped one-expert path of tfm_gather_qmm."""
+    log(f"native_affine_qmm N={N} Kin={Kin} rows={rows}")
+    q, s, b = _weights(1, N, Kin, 7 * N + Kin, gpu)
+    x = wl.normal_bf16((rows, Kin), 1.0, rows + N).to(gpu)
+    out = tmoe.native_affine_qmm(x, q[0], s[0], b[0], 64, 4)
+    grouped = tmoe.gather_qmm_rows(x, q, s, b, torch.zeros(rows, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(out), u16(grouped))
+    sample = np.unique(np.linspace(0, rows - 1, min(rows, 64)).astype(np.int64))
+    ref = oracle.gather_qmm_f64(u16(x)[sample], np.arange(sample.size), np.zeros(sample.size, np.int32),
+                                u32(q), u16(s), u16(b))
+    err = max_rel(oracle.bf16_to_f32(u16(out)[sample]), ref)
+    log(f"  max_rel {err:.2e} over {sample.size} rows")
+    assert err <= BLOCK_TOL
+
+
+@pytest.mark.parametrize("dtype,bits", [("f16", 4), ("bf16", 8), ("f16", 8)])
+@pytest.mark.parametrize("rows", [1, 300])
+def test_native_affine_qmm_dtypes(gpu, dtype, bits, rows):
+    """Half storage and 8-bit codes through tfm_affine_qmm (the grouped GEMM at
+    every row count) against the oracle."""
+    log(f"native_affine_qmm {dtype} bits={bits} rows={rows}")
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    N, Kin = 1024, 2048
+    q = wl.packed_nibbles((N, Kin * bits // 32), 40 + bits, gpu)
+    s = wl.uniform_scales((N, Kin // 64), 41, gpu, lo=0.005 * 16 / 2 ** bits, hi=0.02 * 16 / 2 ** bits,
+                          dtype=tdt)
+    b = (s.float() * -float(2 ** (bits - 1))).to(tdt)
+    x = wl.normal_bf16((rows, Kin), 1.0, 42, dtype=tdt).to(gpu)
+    out = tmoe.native_affine_qmm(x, q, s, b, 64, bits)
+    torch.cuda.synchronize()
+    assert out.dtype == tdt
+    ref = oracle.gather_qmm_f64(u16(x), np.arange(rows), np.zeros(rows, np.int32), u32(q)[None], u16(s)[None],
+                                u16(b)[None], dtype=dtype)
+    err = max_rel(oracle.st_to_f32(u16(out), dtype), ref)
+    log(f"  max_rel {err:.2e}")
+    assert err <= BLOCK_TOL
+
+
 def test_affine_validation_errors(gpu):
     q, s, b = _weights(2, 64, 128, 1, gpu)
     x = torch.zeros((3, 128), dtype=torch.bfloat16, device=gpu)

@@ -17,7 +17,7 @@ and the hook's GPUCallable checked route by route against the oracle.
    against the oracle's per-route chain (fp64 gate and up products of the
    route's token row with its expert, SwiGLU, fp64 down product), with
    caller-order and expert-sorted routes, bf16 and half storage, N = 8 (GEMV
-   kernels for bf16) and N = 2400 (grouped GEMM)."""
+   kernels) and N = 2400 (grouped GEMM)."""
 import json
 import os
 

@@ -109,6 +109,8 @@ SIGNATURES = {
     "tfm_gather_qmm": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, POINTER(Affine),
                                c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                                c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tfm_affine_qmm": (c_int, [c_void_p, c_int64, POINTER(Affine), c_int32, c_int32, c_int32, c_int32,
+                               c_int32, c_void_p, c_void_p]),
     "tfm_moe_experts": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
                                 POINTER(MoeWeights), c_void_p, c_uint32, c_void_p, c_size_t,
                                 c_void_p]),

@@ -185,10 +185,10 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // rather than the grouped GEMM (64-row tiles) up to gemv_threshold() routes.
 
 // Tokens up to which the streaming decode kernels take a batch that the
-// decode GEMV kernels (bf16 storage, 4-bit codes) could also run; past it the
-// GEMV kernels do (TFM_DS_MAX_TOKENS overrides; an affine router is
-// dequantised first on either path). Batches no GEMV kernel runs (half
-// storage, 8-bit codes) stream whenever they fit.
+// decode GEMV kernels (4-bit codes, bf16 or half storage) could also run;
+// past it the GEMV kernels do (TFM_DS_MAX_TOKENS overrides; an affine router
+// is dequantised first on either path). Batches no GEMV kernel runs (8-bit
+// codes) stream whenever they fit.
 // Per layer, streaming against GEMV: OLMoE 1 token 16.8 against 22.4 us,
 // 2 tokens 26.4 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
 // layers) 56.0 against 53.0, 12 tokens 75.6 against 63.2; Granite 1 token
@@ -318,8 +318,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const int64_t R = T * K;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
   const bool small = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
-  // The standalone GEMV kernels (gemv.hip) are 4-bit bf16 only.
-  const bool gemv = small && !f16 && g.bits == 4;
+  // The standalone GEMV kernels (gemv.hip) take 4-bit codes (bf16 or half storage).
+  const bool gemv = small && g.bits == 4;
   // The streaming kernels at the sizes where tfm_moe_forward runs them.
   if (!grouped && fused_decode(g, R) && decode_stream_fits((int)T, K, E, H, I) &&
       ((int)T <= ds_max_tokens() || !gemv)) {
@@ -358,14 +358,14 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   if (gemv) {
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_gemv_gateup(x, rm, ws.grp, max_active, R, w->gate, w->up, I, H, ws.h, s);
+      launch_gemv_gateup(f16, x, rm, ws.grp, max_active, R, w->gate, w->up, I, H, ws.h, s);
     }
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_gemv_scaled(ws.h, ws.grp, max_active, R, w->down, H, I, gates, ws.P, s);
+      launch_gemv_scaled(f16, ws.h, ws.grp, max_active, R, w->down, H, I, gates, ws.P, s);
     }
     StageScope st(TFM_STAGE_COMBINE, s);
-    launch_combine_sorted(false, ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
+    launch_combine_sorted(f16, ws.P, ws.grp.inverse, ws.grp.offsets + E, (int)T, K, H, residual,
                           g.residual_multiplier, y, s);
   } else {
     // Prefill: the down projection writes bf16 expert outputs in sorted
@@ -629,12 +629,46 @@ int tfm_gather_qmm(const void* x, int64_t x_row_count, const int32_t* x_rows,
     // x_rows == nullptr means identity: RowMap uses f / K with K = 1.
     const RowMap rm{ws.grp.order, x_rows, 1, x_row_count, &ws.hdr->status};
     const int max_active = (int)(rows < num_experts ? rows : num_experts);
-    if (bits == 4 && dtype == TFM_DTYPE_BF16 && rows <= gemv_threshold() && k_in <= 2048)
-      launch_gemv_plain(static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
+    if (bits == 4 && rows <= gemv_threshold() && k_in <= 2048)
+      launch_gemv_plain(dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(x), rm, ws.grp, max_active, rows, *w, n_out, k_in,
                         static_cast<uint16_t*>(out), s);
     else
       launch_ggemm_plain(static_cast<const uint16_t*>(x), rm, ws.grp, rows, num_experts, *w, n_out,
                          k_in, bits, dtype == TFM_DTYPE_F16, static_cast<uint16_t*>(out), s);
+  });
+}
+
+int tfm_affine_qmm(const void* x, int64_t rows, const tfm_affine* w, int32_t n_out,
+                   int32_t k_in, int32_t group_size, int32_t bits, int32_t dtype, void* out,
+                   void* stream) {
+  return guarded([&] {
+    need(rows >= 0 && rows <= INT32_MAX, "rows out of range");
+    need(n_out > 0 && k_in > 0, "n_out and k_in must be positive");
+    need(bits == 4 || bits == 8, "bits must be 4 or 8");
+    need(group_size == 32 || group_size == 64 || group_size == 128, "group_size must be 32, 64 or 128");
+    need(k_in % group_size == 0, "k_in must be a multiple of group_size");
+    if (group_size != 64) fail(TFM_E_UNSUPPORTED, "only group_size 64 is built");
+    need(dtype == TFM_DTYPE_BF16 || dtype == TFM_DTYPE_F16, "unknown dtype");
+    if (n_out % 64 != 0) fail(TFM_E_UNSUPPORTED, "n_out must be a multiple of 64");
+    if (rows == 0) return;
+    need_ptr(x, "x");
+    need_ptr(w, "w");
+    need_ptr(out, "out");
+    need_align16(x, "x");
+    check_affine(*w, "w");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // One expert owning every row in caller order: no grouping pass, and no
+    // row can be out of range (the status word is never written).
+    Grouping grp{};
+    grp.E = 1;
+    grp.ident = (int)rows;
+    const RowMap rm{nullptr, nullptr, 1, rows, nullptr};
+    if (bits == 4 && rows <= gemv_threshold() && k_in <= 2048)
+      launch_gemv_plain(dtype == TFM_DTYPE_F16, static_cast<const uint16_t*>(x), rm, grp, 1, rows, *w, n_out, k_in,
+                        static_cast<uint16_t*>(out), s);
+    else
+      launch_ggemm_plain(static_cast<const uint16_t*>(x), rm, grp, rows, 1, *w, n_out, k_in, bits,
+                         dtype == TFM_DTYPE_F16, static_cast<uint16_t*>(out), s);
   });
 }
 
@@ -672,7 +706,7 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
   const int H = g.hidden_size, I = g.intermediate_size;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
-  const bool gemv_decode = fused_decode(g, R) && R <= plan->gemv_max_routes && !f16 && g.bits == 4;
+  const bool gemv_decode = fused_decode(g, R) && R <= plan->gemv_max_routes && g.bits == 4;
   if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I) && (T <= ds_max_tokens() || !gemv_decode)) {
     Grouping gd = ws.grp;
     gd.slots = ws.slots;
@@ -720,10 +754,10 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
       StageScope st(TFM_STAGE_ROUTER, s);
       const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
       if (g.router == TFM_ROUTER_AFFINE) {
-        launch_dequant_router(false, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
+        launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
         rw = ws.router_w;
       }
-      launch_decode_route(g.route, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
+      launch_decode_route(g.route, f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
                           H, E, K, ws.logits, ws.idx, ws.gates, s);
     }
     // The gate/up kernel publishes the grouping with its slot table and
@@ -733,17 +767,17 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
     gd.gates_sorted = ws.gates_sorted;
     {
       StageScope st(TFM_STAGE_GATEUP, s);
-      launch_decode_gateup(static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
+      launch_decode_gateup(f16, static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
                            weights->gate, weights->up, gd, ws.h, &ws.hdr->status, s);
     }
     const int max_active = (int)(R < E ? R : E);
     {
       StageScope st(TFM_STAGE_DOWN, s);
-      launch_gemv_scaled(ws.h, gd, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
+      launch_gemv_scaled(f16, ws.h, gd, max_active, R, weights->down, H, I, ws.gates, ws.P, s);
     }
     {
       StageScope st(TFM_STAGE_COMBINE, s);
-      launch_combine_sorted(false, ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
+      launch_combine_sorted(f16, ws.P, ws.grp.inverse, ws.grp.offsets + E, T, K, H,
                             static_cast<const uint16_t*>(residual), g.residual_multiplier,
                             static_cast<uint16_t*>(y), s);
     }
@@ -922,13 +956,12 @@ int tfm_expert_routes(const tfm_plan* plan, const void* x, int64_t tokens,
     const RowMap rm{grp.order, token_indices, 1, tokens, &hdr->status};
     const int max_active = (int)(n_routes < E ? n_routes : E);
     const uint16_t* xp = static_cast<const uint16_t*>(x);
-    if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048 && g.dtype == TFM_DTYPE_BF16 &&
-        g.bits == 4) {
-      launch_gemv_gateup(xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
-      launch_gemv_scaled(h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
-      launch_rows_to_bf16(P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
+    const bool f16 = g.dtype == TFM_DTYPE_F16;
+    if (n_routes <= plan->gemv_max_routes && H <= 2048 && I <= 2048 && g.bits == 4) {
+      launch_gemv_gateup(f16, xp, rm, grp, max_active, n_routes, weights->gate, weights->up, I, H, h, s);
+      launch_gemv_scaled(f16, h, grp, max_active, n_routes, weights->down, H, I, nullptr, P, s);
+      launch_rows_to_st(f16, P, n_routes, H, static_cast<uint16_t*>(out_sorted), s);
     } else {
-      const bool f16 = g.dtype == TFM_DTYPE_F16;
       launch_ggemm_gateup(xp, rm, grp, n_routes, E, weights->gate, weights->up, I, H, g.bits, f16, h, s);
       launch_ggemm_down(h, grp, n_routes, E, weights->down, H, I, g.bits, f16,
                         static_cast<uint16_t*>(out_sorted), s);

@@ -182,16 +182,21 @@ void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, co
   check_hip(hipGetLastError(), "combine launch");
 }
 
-__global__ void rows_to_bf16_kernel(const float* __restrict__ P, int64_t n, uint16_t* __restrict__ out) {
+template <bool F16>
+__global__ void rows_to_st_kernel(const float* __restrict__ P, int64_t n, uint16_t* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = f2bf(P[i]);
+  if (i < n) out[i] = f2st<F16>(P[i]);
 }
 
-void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s) {
+// fp32 rows rounded to the storage dtype (bf16, or IEEE half when f16).
+void launch_rows_to_st(bool f16, const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s) {
   const int64_t n = rows * H;
   if (n <= 0) return;
-  rows_to_bf16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, n, out);
-  check_hip(hipGetLastError(), "rows_to_bf16 launch");
+  if (f16)
+    rows_to_st_kernel<true><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, n, out);
+  else
+    rows_to_st_kernel<false><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(P, n, out);
+  check_hip(hipGetLastError(), "rows_to_st launch");
 }
 
 __global__ void copy_i32_kernel(const int32_t* __restrict__ a, int32_t* __restrict__ b, int64_t n) {

@@ -44,7 +44,7 @@ __device__ __forceinline__ uint64_t lanemask_lt64() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-template <int LG>
+template <int LG, bool F16>
 __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) {
   __shared__ GemvLds L;
   __shared__ int s_order[kDecodeMaxRoutes];
@@ -131,9 +131,9 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
   auto stage = [&](int, int) {};
   auto emit = [&](int j, int, int n, float gt, float up) {
     const float hv = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
-    h[(int64_t)j * N + n] = f2bf(hv);
+    h[(int64_t)j * N + n] = f2st<F16>(hv);
   };
-  gemv_units<LG, 2, kGemvUnits>(L, A.x, A.H, N, A.gate, A.up, ex, s_off[ex], s_off[ex + 1],
+  gemv_units<LG, 2, kGemvUnits, F16>(L, A.x, A.H, N, A.gate, A.up, ex, s_off[ex], s_off[ex + 1],
                                 blockIdx.x * kGemvUnits, xrow, stage, emit);
 }
 
@@ -251,15 +251,15 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
   check_hip(hipGetLastError(), "decode logits launch");
 }
 
-void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
-                         int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
-                         hipStream_t s) {
+void launch_decode_route(int route_kind, bool f16, const uint16_t* x, const uint16_t* router,
+                         const float* bias, int T, int H, int E, int K, uint16_t* logits, int32_t* idx,
+                         float* gates, hipStream_t s) {
   if (T <= 0) return;
-  launch_decode_logits(false, x, router, bias, T, H, E, logits, s);
-  launch_topk(route_kind, false, logits, T, E, K, idx, nullptr, gates, s);
+  launch_decode_logits(f16, x, router, bias, T, H, E, logits, s);
+  launch_topk(route_kind, f16, logits, T, E, K, idx, nullptr, gates, s);
 }
 
-void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
+void launch_decode_gateup(bool f16, const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
                           int K, int H, int I, const tfm_affine& gate, const tfm_affine& up,
                           const Grouping& g, uint16_t* h, uint32_t* status, hipStream_t s) {
   if (!g.slots || !g.gates_sorted) fail(TFM_E_INVALID, "decode gate/up: slot table missing");
@@ -274,13 +274,21 @@ void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* ga
   const int ur = 4 * (64 / lg), upe = (I + ur - 1) / ur;
   const int max_active = T * K < E ? T * K : E;
   const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active);
-  switch (lg) {
-    case 4: tfm_launch(decode_gateup_kernel<4>, grid, 256, 0, s, A); break;
-    case 8: tfm_launch(decode_gateup_kernel<8>, grid, 256, 0, s, A); break;
-    case 16: tfm_launch(decode_gateup_kernel<16>, grid, 256, 0, s, A); break;
-    case 32: tfm_launch(decode_gateup_kernel<32>, grid, 256, 0, s, A); break;
-    default: tfm_launch(decode_gateup_kernel<64>, grid, 256, 0, s, A); break;
+#define TFM_DECODE_GU(LGV)                                                  \
+  {                                                                         \
+    if (f16)                                                                \
+      tfm_launch(decode_gateup_kernel<LGV, true>, grid, 256, 0, s, A);      \
+    else                                                                    \
+      tfm_launch(decode_gateup_kernel<LGV, false>, grid, 256, 0, s, A);     \
   }
+  switch (lg) {
+    case 4: TFM_DECODE_GU(4) break;
+    case 8: TFM_DECODE_GU(8) break;
+    case 16: TFM_DECODE_GU(16) break;
+    case 32: TFM_DECODE_GU(32) break;
+    default: TFM_DECODE_GU(64) break;
+  }
+#undef TFM_DECODE_GU
   check_hip(hipGetLastError(), "decode gate/up launch");
 }
 

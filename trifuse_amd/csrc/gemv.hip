@@ -26,7 +26,7 @@ namespace tfm {
 // Standalone decode GEMV over grouped routes (gather_qmm and the MoE block
 // given routes): workgroup (bx, a) (4 waves) streams kGemvUnits row units of
 // active expert a (blockIdx.y indexes the ascending active-expert list).
-template <int LG, int MODE>
+template <int LG, int MODE, bool F16>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x, RowMap rm,
                                                    Grouping g, tfm_affine wa, tfm_affine wb,
                                                    int N, int kin, const float* __restrict__ gates,
@@ -45,35 +45,35 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     j0 = sl.y;
     j1 = sl.z;
   } else {
-    if ((int)blockIdx.y >= g.active[g.E]) return;
-    e = g.active[blockIdx.y];
-    j0 = g.offsets[e];
-    j1 = g.offsets[e + 1];
+    if ((int)blockIdx.y >= grp_active_count(g)) return;
+    e = grp_active_id(g, blockIdx.y);
+    j0 = grp_offset(g, e);
+    j1 = grp_offset(g, e + 1);
   }
   auto xrow = [&](int j) -> int64_t { return MODE == kScaled ? (int64_t)j : route_row(rm, j); };
   auto stage = [&](int jb, int nb) {
     const int t = threadIdx.x;
     if (t < nb) {
       if (MODE == kScaled)
-        xgate[t] = g.gates_sorted ? g.gates_sorted[jb + t] : gates ? gates[rm.order[jb + t]] : 1.0f;
-      if (MODE == kPlain) xorow[t] = rm.order[jb + t];
+        xgate[t] = g.gates_sorted ? g.gates_sorted[jb + t] : gates ? gates[route_flat(rm, jb + t)] : 1.0f;
+      if (MODE == kPlain) xorow[t] = route_flat(rm, jb + t);
     }
   };
   auto emit = [&](int j, int t, int n, float a0, float a1) {
     if (MODE == kGateUp) {
       const float hv = a0 * __builtin_amdgcn_rcpf(1.0f + __expf(-a0)) * a1;
-      static_cast<uint16_t*>(out)[(int64_t)j * N + n] = f2bf(hv);
+      static_cast<uint16_t*>(out)[(int64_t)j * N + n] = f2st<F16>(hv);
     } else if (MODE == kPlain) {
-      static_cast<uint16_t*>(out)[(int64_t)xorow[t] * N + n] = f2bf(a0);
+      static_cast<uint16_t*>(out)[(int64_t)xorow[t] * N + n] = f2st<F16>(a0);
     } else {
       static_cast<float*>(out)[(int64_t)j * N + n] = a0 * xgate[t];
     }
   };
-  gemv_units<LG, NM, kGemvUnits>(L, x, kin, N, wa, wb, e, j0, j1, blockIdx.x * kGemvUnits, xrow, stage,
+  gemv_units<LG, NM, kGemvUnits, F16>(L, x, kin, N, wa, wb, e, j0, j1, blockIdx.x * kGemvUnits, xrow, stage,
                                  emit);
 }
 
-template <int MODE>
+template <int MODE, bool F16>
 static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
                           const tfm_affine& wa, const tfm_affine& wb, int N, const float* gates,
                           void* out, hipStream_t s) {
@@ -85,7 +85,7 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   {                                                                                         \
     const int ur = 4 * (64 / LGV), upe = (N + ur - 1) / ur;                                 \
     const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active); \
-    tfm_launch(gemv_kernel<LGV, MODE>, grid, 256, 0, s, x, rm, g, wa, wb, N, Kin, gates, out);      \
+    tfm_launch(gemv_kernel<LGV, MODE, F16>, grid, 256, 0, s, x, rm, g, wa, wb, N, Kin, gates, out); \
   }
   if (nch <= 4) TFM_GEMV_LAUNCH(4)
   else if (nch <= 8) TFM_GEMV_LAUNCH(8)
@@ -96,26 +96,35 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   check_hip(hipGetLastError(), "gemv launch");
 }
 
-void launch_gemv_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+void launch_gemv_gateup(bool f16, const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
                         int64_t routes, const tfm_affine& gate, const tfm_affine& up, int N,
                         int Kin, uint16_t* h, hipStream_t s) {
   (void)routes;
-  dispatch_gemv<kGateUp>(Kin, x, rm, g, max_active, gate, up, N, nullptr, h, s);
+  if (f16)
+    dispatch_gemv<kGateUp, true>(Kin, x, rm, g, max_active, gate, up, N, nullptr, h, s);
+  else
+    dispatch_gemv<kGateUp, false>(Kin, x, rm, g, max_active, gate, up, N, nullptr, h, s);
 }
 
-void launch_gemv_plain(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+void launch_gemv_plain(bool f16, const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
                        int64_t routes, const tfm_affine& w, int N, int Kin, uint16_t* out,
                        hipStream_t s) {
   (void)routes;
-  dispatch_gemv<kPlain>(Kin, x, rm, g, max_active, w, w, N, nullptr, out, s);
+  if (f16)
+    dispatch_gemv<kPlain, true>(Kin, x, rm, g, max_active, w, w, N, nullptr, out, s);
+  else
+    dispatch_gemv<kPlain, false>(Kin, x, rm, g, max_active, w, w, N, nullptr, out, s);
 }
 
-void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_active,
+void launch_gemv_scaled(bool f16, const uint16_t* hsorted, const Grouping& g, int max_active,
                         int64_t routes, const tfm_affine& w, int N, int Kin, const float* gates,
                         float* P, hipStream_t s) {
   (void)routes;
   RowMap rm{g.order, nullptr, 1, 0, nullptr};
-  dispatch_gemv<kScaled>(Kin, hsorted, rm, g, max_active, w, w, N, gates, P, s);
+  if (f16)
+    dispatch_gemv<kScaled, true>(Kin, hsorted, rm, g, max_active, w, w, N, gates, P, s);
+  else
+    dispatch_gemv<kScaled, false>(Kin, hsorted, rm, g, max_active, w, w, N, gates, P, s);
 }
 
 }  // namespace tfm

@@ -152,7 +152,7 @@ struct GemvLds {
 //   emit(j, t, n, a0, a1)  called by the lane holding row n's totals for route
 //                      j (batch slot t); a1 = a0 unless NM = 2.
 // Every thread of the workgroup must call it (it contains barriers).
-template <int LG, int NM, int NU, typename XRow, typename Stage, typename Emit>
+template <int LG, int NM, int NU, bool F16, typename XRow, typename Stage, typename Emit>
 __device__ __forceinline__ void gemv_units(GemvLds& L, const uint16_t* __restrict__ x, int kin, int N,
                                            const tfm_affine& wa, const tfm_affine& wb, int e, int j0,
                                            int j1, int rc0, XRow xrow, Stage stage, Emit emit) {
@@ -200,7 +200,7 @@ __device__ __forceinline__ void gemv_units(GemvLds& L, const uint16_t* __restric
     for (int p = tid; p < nb * nch; p += 256) {
       const int t = p / nch, c = p % nch;
       ChunkX cx;
-      load_x(x + xrow(jb + t) * kin + 32 * c, cx);
+      load_x<F16>(x + xrow(jb + t) * kin + 32 * c, cx);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         L.xs[t][q][c] = make_uint4(cx.p[4 * q], cx.p[4 * q + 1], cx.p[4 * q + 2], cx.p[4 * q + 3]);
@@ -214,10 +214,10 @@ __device__ __forceinline__ void gemv_units(GemvLds& L, const uint16_t* __restric
       float sc[NM], cc[NM];
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        sc[m] = bf2f((uint16_t)cur[m].s);
-        cc[m] = __builtin_fmaf(-128.0f, sc[m], bf2f((uint16_t)cur[m].b));
+        sc[m] = st2f<F16>((uint16_t)cur[m].s);
+        cc[m] = __builtin_fmaf(-code_base(F16), sc[m], st2f<F16>((uint16_t)cur[m].b));
       }
-      // One packed word at a time: its (128+q) pairs for every matrix, then
+      // One packed word at a time: its (base+q) pairs for every matrix, then
       // their dot products with the staged x of every route of the batch.
       float d0[kGemvXB][NM], d1[kGemvXB][NM];
 #pragma unroll
@@ -228,17 +228,17 @@ __device__ __forceinline__ void gemv_units(GemvLds& L, const uint16_t* __restric
       for (int q = 0; q < 4; ++q) {
         uint32_t qp[NM][4];
 #pragma unroll
-        for (int m = 0; m < NM; ++m) unpack_word(word_of(cur[m].q, q), qp[m]);
+        for (int m = 0; m < NM; ++m) unpack_word_st<F16>(word_of(cur[m].q, q), qp[m]);
 #pragma unroll
         for (int t = 0; t < kGemvXB; ++t) {
           if (t < nb) {
             const uint4 v = L.xs[t][q][ll];
 #pragma unroll
             for (int m = 0; m < NM; ++m) {
-              d0[t][m] = dot2(qp[m][0], v.x, d0[t][m]);
-              d1[t][m] = dot2(qp[m][1], v.y, d1[t][m]);
-              d0[t][m] = dot2(qp[m][2], v.z, d0[t][m]);
-              d1[t][m] = dot2(qp[m][3], v.w, d1[t][m]);
+              d0[t][m] = dot2_st<F16>(qp[m][0], v.x, d0[t][m]);
+              d1[t][m] = dot2_st<F16>(qp[m][1], v.y, d1[t][m]);
+              d0[t][m] = dot2_st<F16>(qp[m][2], v.z, d0[t][m]);
+              d1[t][m] = dot2_st<F16>(qp[m][3], v.w, d1[t][m]);
             }
           }
         }

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   if (tid < 64) {
     int t = 0;
     if (tid < E) {
-      const int cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
+      const int cnt = grp_offset(args.g, tid + 1) - grp_offset(args.g, tid);
       t = (cnt + BM - 1) / BM;
     }
 #pragma unroll
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
   if (tid < E && s_tiles[tid] <= mt && mt < s_tiles[tid + 1]) s_expert = tid;
   __syncthreads();
   const int e = s_expert;
-  const int seg0 = args.g.offsets[e], seg1 = args.g.offsets[e + 1];
+  const int seg0 = grp_offset(args.g, e), seg1 = grp_offset(args.g, e + 1);
   const int m0 = seg0 + (mt - s_tiles[e]) * BM;
   const int rows_valid = min(BM, seg1 - m0);
   const int n0 = nt * C::OUT_COLS;
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(WAVES_M_ * WAVES_N_ * 64, 1) void ggemm_kernel(GgAr
       if (c < 32 * CPR && rr < rows_valid && n < args.N) {
         const uint4 v = *reinterpret_cast<const uint4*>(&stage[row * C::SROW + part * 8]);
         const int j = m0 + rr;
-        const int64_t orow = MODE == kGgPlain ? (int64_t)args.rm.order[j] : (int64_t)j;
+        const int64_t orow = MODE == kGgPlain ? (int64_t)route_flat(args.rm, j) : (int64_t)j;
         *reinterpret_cast<uint4*>(&args.out[orow * args.N + n]) = v;
       }
     }
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
   constexpr int CF = BAL ? 13 + MB : 1;
   if (tid < 64) {
     int cnt = 0;
-    if (tid < E) cnt = args.g.offsets[tid + 1] - args.g.offsets[tid];
+    if (tid < E) cnt = grp_offset(args.g, tid + 1) - grp_offset(args.g, tid);
     const int full = cnt / BM, part = cnt % BM;
     const int cp = part > 0 ? (BAL ? 13 + min(MB, ((part + 63) / 64) * 4) : 1) : 0;
     const int mt_e = full + (part > 0 ? 1 : 0);
@@ -631,7 +631,7 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
   if (tid < E && s_tiles[tid] <= mt && mt < s_tiles[tid + 1]) s_expert = tid;
   __syncthreads();
   const int e = s_expert;
-  const int seg0 = args.g.offsets[e], seg1 = args.g.offsets[e + 1];
+  const int seg0 = grp_offset(args.g, e), seg1 = grp_offset(args.g, e + 1);
   const int m0 = seg0 + (mt - s_tiles[e]) * BM;
   const int rows_valid = min(BM, seg1 - m0);
   const int n0 = nt * OUT_COLS;
@@ -895,7 +895,7 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
         const uint16_t* st = (row < HALF_ROWS ? sA0 : sA1) + (row % HALF_ROWS) * SROW;
         const uint4 v = *reinterpret_cast<const uint4*>(&st[part * 8]);
         const int j = m0 + row;
-        const int64_t orow = MODE == kGgPlain ? (int64_t)args.rm.order[j] : (int64_t)j;
+        const int64_t orow = MODE == kGgPlain ? (int64_t)route_flat(args.rm, j) : (int64_t)j;
         *reinterpret_cast<uint4*>(&args.out[orow * args.N + n]) = v;
       }
     }
@@ -943,12 +943,22 @@ static int gg_device_cus() {
 //    128-row tiles do not (Granite, 4 gate/up column tiles: 768 tokens,
 //    a = 154, 84.4 against 98.6 us; at 512 tokens both fit, and 128-row tiles
 //    win, 70.7 against 73.1);
-//  * else 128.
+//  * else 128;
+//  * with few experts and output columns (E x col_tiles below a quarter of
+//    the compute units: a dense matrix, E = 1), the largest tile whose count
+//    fills the compute units, else 64 (OLMoE q_proj at 512 rows has 16
+//    256-row tiles and 64 64-row ones).
 // col_tiles: 256-row weight tiles across the output (gate/up: gate and up
 // rows together).
 static int wr_tile_rows(int64_t n_routes, int E, int64_t col_tiles) {
   const int o = tile_override();
   if (o == 64 || o == 128 || o == 256) return o;
+  if (4 * E * col_tiles < gg_device_cus()) {
+    const int64_t cus = gg_device_cus();
+    for (int bm = 256; bm >= 128; bm /= 2)
+      if ((n_routes + (int64_t)E * bm - 1) / ((int64_t)E * bm) * E * col_tiles >= cus) return bm;
+    return 64;
+  }
   if (n_routes <= (int64_t)E * 56) return 64;
   if (n_routes >= (int64_t)E * 208) return 256;
   const int64_t m128 = (n_routes + (int64_t)E * 128 - 1) / ((int64_t)E * 128);

@@ -37,26 +37,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // Float to IEEE half bits, round to nearest even (subnormal results included,
-// overflow to infinity, NaN kept quiet with its sign). Integer arithmetic, so
-// the result does not depend on the hardware denormal mode.
-__device__ __forceinline__ uint16_t f2h(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 16) & 0x8000u;
-  const uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
-  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // |f| >= 65520 rounds to infinity
-  if (a >= 0x38800000u) {                                    // normal half: rebias 127 -> 15
-    const uint32_t r = a - 0x38000000u;
-    return (uint16_t)(sign | ((r + 0xfffu + ((r >> 13) & 1u)) >> 13));
-  }
-  if (a <= 0x33000000u) return (uint16_t)sign;               // |f| <= 2^-25 rounds to zero
-  const uint32_t m = (a & 0x7fffffu) | 0x800000u;            // subnormal half: units of 2^-24
-  const int sh = 126 - (int)(a >> 23);                       // 14 .. 24
-  uint32_t q = m >> sh;
-  const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
-  q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
-  return (uint16_t)(sign | q);
-}
+// overflow to infinity, NaN kept quiet with its sign): one v_cvt_f16_f32.
+// Every kernel of the library runs with round-to-nearest-even and f32 and
+// f16 denormals preserved (the code object's default float mode), so the
+// conversion is the IEEE one. It has no branches: a branchy integer version
+// in the GEMV epilogues kept the compiler from moving loads and dot products
+// across it.
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // Activation storage of the block: bf16 (F16 = false) or IEEE half, as bits.
 template <bool F16>

@@ -80,7 +80,19 @@ struct Grouping {
   // sorted order.
   int4* slots;          // [E]
   float* gates_sorted;  // [n]
+  // ident > 0: the identity grouping of a dense matrix (E == 1): expert 0
+  // owns routes [0, ident) in caller order, and order, inverse, offsets and
+  // active are not read (they may be null).
+  int ident;
 };
+
+// Segment start of expert e (e <= E), the active-expert count and the id of
+// active slot a, for both a written grouping and the identity one.
+__device__ __forceinline__ int grp_offset(const Grouping& g, int e) {
+  return g.ident ? (e == 0 ? 0 : g.ident) : g.offsets[e];
+}
+__device__ __forceinline__ int grp_active_count(const Grouping& g) { return g.ident ? 1 : g.active[g.E]; }
+__device__ __forceinline__ int grp_active_id(const Grouping& g, int a) { return g.ident ? 0 : g.active[a]; }
 
 // ---- launchers (defined in the .hip files) ----
 void launch_router_logits(bool f16, const uint16_t* x, const uint16_t* w, const float* bias, int T,
@@ -124,7 +136,7 @@ void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, i
                     uint16_t* out, hipStream_t s);
 
 // Decode path (decode.hip), T*K <= 256 routes.
-void launch_decode_route(int route_kind, const uint16_t* x, const uint16_t* router, const float* bias,
+void launch_decode_route(int route_kind, bool f16, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s);
 void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, const float* bias, int T,
@@ -220,12 +232,13 @@ inline void launch_ds_route_group(bool f16, int route_kind, const uint16_t* logi
 #undef TFM_DS_PICK
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
-void launch_decode_gateup(const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
+void launch_decode_gateup(bool f16, const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
                           int K, int H, int I, const tfm_affine& gate, const tfm_affine& up,
                           const Grouping& g, uint16_t* h, uint32_t* status, hipStream_t s);
 
 // Row source of a sorted route j: x row = x_rows ? x_rows[order[j]] : order[j] / K.
 // Rows outside [0, nx) are read as row 0 and flag TFM_STATUS_BAD_ROW_INDEX.
+// A null order is the identity (the dense matrix of an identity grouping).
 struct RowMap {
   const int32_t* order;
   const int32_t* x_rows;  // may be null
@@ -234,8 +247,10 @@ struct RowMap {
   uint32_t* status;       // workspace status word
 };
 
+__device__ __forceinline__ int route_flat(const RowMap& rm, int j) { return rm.order ? rm.order[j] : j; }
+
 __device__ __forceinline__ int64_t route_row(const RowMap& rm, int j) {
-  const int f = rm.order[j];
+  const int f = route_flat(rm, j);
   int64_t r = rm.x_rows ? (int64_t)rm.x_rows[f] : (int64_t)(f / rm.K);
   if (r < 0 || r >= rm.nx) {
     atomicOr(rm.status, (uint32_t)TFM_STATUS_BAD_ROW_INDEX);
@@ -245,17 +260,18 @@ __device__ __forceinline__ int64_t route_row(const RowMap& rm, int j) {
 }
 
 // Decode-style (few routes per expert) dequant GEMV family.
-//   gateup: h[j, n] = bf16(silu(xg) * xu)            (sorted route j)
-//   plain:  out[order[j], n] = bf16(x . w)            (gather_qmm)
+//   gateup: h[j, n] = st(silu(xg) * xu)              (sorted route j)
+//   plain:  out[order[j], n] = st(x . w)              (gather_qmm)
 //   scaled: P[j, n] = (x . w) * gate[order[j]]        (fp32, down + combine)
+// st: the storage dtype (bf16, or IEEE half when f16); 4-bit codes.
 // `routes` is the total route count (sizes the per-pass route batch).
-void launch_gemv_gateup(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+void launch_gemv_gateup(bool f16, const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
                         int64_t routes, const tfm_affine& gate, const tfm_affine& up, int N,
                         int Kin, uint16_t* h, hipStream_t s);
-void launch_gemv_plain(const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
+void launch_gemv_plain(bool f16, const uint16_t* x, RowMap rm, const Grouping& g, int max_active,
                        int64_t routes, const tfm_affine& w, int N, int Kin, uint16_t* out,
                        hipStream_t s);
-void launch_gemv_scaled(const uint16_t* hsorted, const Grouping& g, int max_active,
+void launch_gemv_scaled(bool f16, const uint16_t* hsorted, const Grouping& g, int max_active,
                         int64_t routes, const tfm_affine& w, int N, int Kin, const float* gates,
                         float* P, hipStream_t s);
 
@@ -286,7 +302,7 @@ void launch_combine_rows(bool f16, const uint16_t* Y, const int32_t* inverse, co
                          const float* gates, int T, int K, int H, const uint16_t* residual,
                          float rmul, uint16_t* y, hipStream_t s);
 // Expert-sorted output rows for the hook (decode path): out[j, c] = bf16(P[j, c])
-void launch_rows_to_bf16(const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s);
+void launch_rows_to_st(bool f16, const float* P, int64_t rows, int H, uint16_t* out, hipStream_t s);
 void launch_copy_i32(const int32_t* src, int32_t* dst, int64_t n, hipStream_t s);
 
 }  // namespace tfm

@@ -214,12 +214,16 @@ def native_affine_qmm(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, bi
     width = validate_affine(q, scales, biases, group_size, bits, 2)
     if x.ndim < 1 or x.shape[-1] != width or x.dtype != scales.dtype:
         raise ValueError("Native affine QMM input width/dtype differs")
+    _dev(x, "x")
     lead = x.shape[:-1]
     rows = x.reshape(-1, width).contiguous()
-    zeros = torch.zeros(rows.shape[0], dtype=torch.int32, device=x.device)
-    out = gather_qmm_rows(rows, q.unsqueeze(0).contiguous(), scales.unsqueeze(0).contiguous(),
-                          biases.unsqueeze(0).contiguous(), zeros, None, True, group_size, bits)
-    return out.reshape(*lead, q.shape[-2])
+    N = q.shape[-2]
+    out = torch.empty((rows.shape[0], N), dtype=x.dtype, device=x.device)
+    qc, sc, bc = q.contiguous(), scales.contiguous(), biases.contiguous()  # alive through the call
+    aff = _affine(qc, sc, bc)
+    call("tfm_affine_qmm", rows.data_ptr(), rows.shape[0], ctypes.byref(aff), N, width, group_size, bits,
+         _dtype_code(x, "x"), out.data_ptr(), _stream())
+    return out.reshape(*lead, N)
 
 
 def native_olmoe_softmax(x: torch.Tensor) -> torch.Tensor:
