@@ -550,13 +550,20 @@ __device__ __forceinline__ f32x4_t mfma16(f16x8_t a, f16x8_t b, f32x4_t c, std::
 
 // BM = 64 (few routes per expert): 64 KB of LDS and 32 accumulator
 // registers, so two workgroups share a compute unit and each covers the
-// other's weight-load latency, which a super-step's few MFMAs cannot.
-template <int BM, int MODE, bool F16>
-__global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs args) {
-  constexpr int WAVES = 8, BN = 256;
+// other's weight-load latency, which a super-step's few MFMAs cannot. WV = 4
+// (64-row tiles only) halves the weight rows of a tile (128: 64 gate and 64
+// up rows, or 128 down rows) for twice the tiles, where 8-wave tiles would
+// leave compute units idle (a few experts or a few output columns: Granite
+// decode batches, a dense matrix); 48 KB of LDS, three workgroups per
+// compute unit.
+template <int BM, int MODE, bool F16, int WV>
+__global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void ggemm_wr_kernel(GgArgs args) {
+  constexpr int WAVES = WV, BN = 32 * WV;
   constexpr int MB = BM / 16;                     // 16-row blocks per wave
   constexpr int OUT_COLS = MODE == kGgGateUp ? BN / 2 : BN;
-  constexpr int LA = BM / 32;                     // 4-row (1 KB) copies per wave per super-step
+  constexpr int LA = BM / (4 * WAVES);            // 4-row (1 KB) copies per wave per super-step
+  static_assert(WV == 8 || (WV == 4 && BM == 64), "8 waves, or 4 with 64-row tiles");
+  static_assert(LA >= 1, "every wave copies activation rows");
   constexpr int SROW = 136;                       // epilogue staging row stride (128 columns + 16 B)
   constexpr int HALF_ROWS = BM / 2;               // staged rows per activation stage
   static_assert(BM == 64 || BM == 128 || BM == 256, "tile rows");
@@ -639,9 +646,9 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
   const int G = args.Kin / BK;                    // quantisation groups per row
 
   // ---- activations: global -> LDS ----
-  // Copy i of wave w: rows 4 (8 i + w) .. + 3 (copy i of all waves together:
-  // rows 32 i .. 32 i + 31); lane l writes slot l % 16 of row
-  // 4 (8 i + w) + l / 16, which holds chunk (l % 16) ^ (row & 15).
+  // Copy i of wave w: rows 4 (WAVES i + w) .. + 3 (copy i of all waves
+  // together: rows 4 WAVES i .. + 4 WAVES - 1); lane l writes slot l % 16 of
+  // row 4 (WAVES i + w) + l / 16, which holds chunk (l % 16) ^ (row & 15).
   const __amdgpu_buffer_rsrc_t ra = gg_rsrc(args.x, args.x_bytes);
   const __amdgpu_buffer_rsrc_t rnull = gg_rsrc(args.x, 0);
   uint32_t a_off[LA];
@@ -677,7 +684,7 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const tfm_affine& bm = (MODE == kGgGateUp && j == 1) ? args.wb : args.wa;
-    trow[j] = MODE == kGgGateUp ? j * 128 + 16 * wave + (lane & 15) : 32 * wave + 16 * j + (lane & 15);
+    trow[j] = MODE == kGgGateUp ? j * (BN / 2) + 16 * wave + (lane & 15) : 32 * wave + 16 * j + (lane & 15);
     const int bn = MODE == kGgGateUp ? n0 + 16 * wave + (lane & 15) : n0 + 32 * wave + 16 * j + (lane & 15);
     rbq[j] = gg_rsrc(reinterpret_cast<const char*>(bm.q) + (size_t)e * args.N * qrow, (uint32_t)args.N * qrow);
     b_qoff[j] = bn < args.N ? (uint32_t)bn * qrow + 16u * g4 : kOob;
@@ -753,7 +760,8 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
                      int ktn) __attribute__((always_inline)) {
     constexpr int MBL = decltype(mbl_tag)::value;
     constexpr int NQ = 4 * MBL, D = 3, R = D + 1;
-    constexpr int NC = (16 * MBL + 31) / 32 < LA ? (16 * MBL + 31) / 32 : LA;
+    constexpr int CR = 4 * WAVES;  // rows per copy round
+    constexpr int NC = (16 * MBL + CR - 1) / CR < LA ? (16 * MBL + CR - 1) / CR : LA;
     constexpr int STEP = NQ / (2 * NC) > 0 ? NQ / (2 * NC) : 1;
     static_assert(STEP * (NC - 1) < NQ, "every copy is issued");
     op_t af[R];
@@ -859,11 +867,16 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
   }
 
   // ---- epilogue ----
-  // Rows staged row-major, 128 columns per pass (the first BM/2 rows in
-  // stage 0, the rest in stage 1), then written as 16-byte row pieces. Gate/up: one
-  // pass (wave w holds columns 16w..16w+15 after SwiGLU); down and plain:
-  // two passes, waves 4p..4p+3 staging columns 128p..128p+127.
-  constexpr int PASSES = MODE == kGgGateUp ? 1 : 2;
+  // Rows staged row-major, CP columns per pass (the first BM/2 rows in
+  // stage 0, the rest in stage 1), then written as 16-byte row pieces.
+  // Gate/up: one pass of BN/2 columns (wave w holds columns 16w..16w+15
+  // after SwiGLU); down and plain: BN/128 passes of 128 columns, waves
+  // 4p..4p+3 staging columns 128p..128p+127.
+  constexpr int PASSES = MODE == kGgGateUp ? 1 : BN / 128;
+  constexpr int CP = MODE == kGgGateUp ? BN / 2 : 128;
+  constexpr int PARTS = CP / 8;                   // 16-byte pieces per staged row
+  constexpr int RPI = WAVES * 64 / PARTS;         // rows written per iteration
+  static_assert(CP + 8 <= SROW, "staged row fits its stride");
   static_for<0, PASSES>([&](auto p_) {
     constexpr int p = decltype(p_)::value;
     if (p > 0) __syncthreads();  // the previous pass's reads are done
@@ -886,11 +899,11 @@ __global__ __launch_bounds__(512, BM == 64 ? 2 : 1) void ggemm_wr_kernel(GgArgs 
       });
     }
     __syncthreads();
-    const int part = tid & 15;
-    const int n = n0 + 128 * p + part * 8;
+    const int part = tid % PARTS;
+    const int n = n0 + CP * p + part * 8;
 #pragma unroll
-    for (int r0i = 0; r0i < BM; r0i += 32) {
-      const int row = r0i + (tid >> 4);
+    for (int r0i = 0; r0i < BM; r0i += RPI) {
+      const int row = r0i + tid / PARTS;
       if (row < rows_valid && n < args.N) {
         const uint16_t* st = (row < HALF_ROWS ? sA0 : sA1) + (row % HALF_ROWS) * SROW;
         const uint4 v = *reinterpret_cast<const uint4*>(&st[part * 8]);
@@ -987,18 +1000,47 @@ static void launch_one(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) 
     tfm_launch(ggemm_kernel<BM_, BN_, WAVES_M, WAVES_N, MODE, BITS, F16, false>, grid_for(n_routes, E, BM_, NT), C::THREADS, 0, s, a);
 }
 
-// 4-bit weights, inputs up to 2048 wide and a multiple of 128: weights in
-// registers (ggemm_wr_kernel); otherwise ggemm_kernel.
-template <int BM, int MODE, bool F16>
-static void launch_wr(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
-  constexpr int OUT_COLS = MODE == kGgGateUp ? 128 : 256;
+// Waves per workgroup of the 64-row weights-in-registers tiles
+// (TFM_GGEMM_WAVES=4/8 forces one): 4 (tiles of half the weight rows) while
+// 8-wave tiles number fewer than two per compute unit, else 8. Per layer, 4
+// against 8 waves: Granite decode 32 38.9 against 40.7 us, Granite 64 tokens
+// 40.8 against 42.5; OLMoE 32 tokens (over two tiles per compute unit) 85.7
+// against 75.2. Two-wave tiles measured no faster than four (Granite decode
+// 32: 40.2 us).
+static int wr_waves(int64_t tiles8) {
+  static const int o = [] {
+    const char* s = std::getenv("TFM_GGEMM_WAVES");
+    return s ? std::atoi(s) : 0;
+  }();
+  if (o == 4 || o == 8) return o;
+  return tiles8 < 2 * (int64_t)gg_device_cus() ? 4 : 8;
+}
+
+template <int BM, int MODE, bool F16, int WV>
+static void launch_wr_waves(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  constexpr int OUT_COLS = MODE == kGgGateUp ? 16 * WV : 32 * WV;
   const int NT = (a.N + OUT_COLS - 1) / OUT_COLS;
   // With 256-row tiles an XCD's run of cheap tiles holds more tiles than an
   // even share: at most share x 29 / 17 + 2 (full tile 29 units, cheapest
   // 17); workgroups past their XCD's run exit at once.
   unsigned grid = grid_for(n_routes, E, BM, NT);
   if (BM == 256) grid = ((grid / 8 * 29 + 16) / 17 + 2) * 8;
-  tfm_launch(ggemm_wr_kernel<BM, MODE, F16>, grid, 512, 0, s, a);
+  tfm_launch(ggemm_wr_kernel<BM, MODE, F16, WV>, grid, WV * 64, 0, s, a);
+}
+
+// 4-bit weights, inputs up to 2048 wide and a multiple of 128: weights in
+// registers (ggemm_wr_kernel); otherwise ggemm_kernel.
+template <int BM, int MODE, bool F16>
+static void launch_wr(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+  if constexpr (BM == 64) {
+    constexpr int OUT8 = MODE == kGgGateUp ? 128 : 256;
+    const int wv = wr_waves(grid_for(n_routes, E, BM, (a.N + OUT8 - 1) / OUT8));
+    if (wv == 4) {
+      launch_wr_waves<BM, MODE, F16, 4>(a, n_routes, E, s);
+      return;
+    }
+  }
+  launch_wr_waves<BM, MODE, F16, 8>(a, n_routes, E, s);
 }
 
 template <int MODE, int BITS, bool F16>
