@@ -62,16 +62,30 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
       wv[8 * i + 6] = lo_st<F16>(v.w); wv[8 * i + 7] = hi_st<F16>(v.w);
     }
     const float be = bias ? bias[e] : 0.0f;
+    if constexpr (TW == 4) {
+      float s[4];
 #pragma unroll
-    for (int t = 0; t < TW; ++t) {
-      float s = 0.0f;
+      for (int t = 0; t < 4; ++t) {
+        s[t] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
-      s = wave_tree_sum64(s);
-      const int tok = tt * TW + t;
-      if (lane == 63 && tok < T) {
-        const float v = bias ? s + be : s;
-        logits[(int64_t)tok * E + e] = f2st<F16>(v);
+        for (int j = 0; j < C; ++j) s[t] = __builtin_fmaf(xv[t][j], wv[j], s[t]);
+      }
+      // Row t of the wave holds token t's logit.
+      const float r = wave_tree_sum64x4(s[0], s[1], s[2], s[3]);
+      const int tok = tt * 4 + (lane >> 4);
+      if ((lane & 15) == 0 && tok < T) logits[(int64_t)tok * E + e] = f2st<F16>(bias ? r + be : r);
+    } else {
+#pragma unroll
+      for (int t = 0; t < TW; ++t) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
+        s = wave_tree_sum64(s);
+        const int tok = tt * TW + t;
+        if (lane == 63 && tok < T) {
+          const float v = bias ? s + be : s;
+          logits[(int64_t)tok * E + e] = f2st<F16>(v);
+        }
       }
     }
   }
@@ -137,14 +151,16 @@ __global__ __launch_bounds__(W * 64) void router_topk_kernel(const uint16_t* __r
       wv[8 * i + 6] = lo_st<F16>(r[i].w); wv[8 * i + 7] = hi_st<F16>(r[i].w);
     }
     const float be = bias ? bias[e] : 0.0f;
+    float s[TB];
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
-      float s = 0.0f;
+      s[t] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < C; ++j) s = __builtin_fmaf(xv[t][j], wv[j], s);
-      s = wave_tree_sum64(s);
-      if (lane == 63) s_logit[t][e] = f2st<F16>(bias ? s + be : s);
+      for (int j = 0; j < C; ++j) s[t] = __builtin_fmaf(xv[t][j], wv[j], s[t]);
     }
+    // Row t of the wave holds token t's logit.
+    const float lg = wave_tree_sum64x4(s[0], s[1], s[2], s[3]);
+    if ((lane & 15) == 0) s_logit[lane >> 4][e] = f2st<F16>(bias ? lg + be : lg);
   };
   const int epw = (E + W - 1) / W;
   const int e0 = wave * epw, e1 = min(E, e0 + epw);

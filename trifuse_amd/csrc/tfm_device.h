@@ -137,6 +137,35 @@ __device__ __forceinline__ float wave_tree_sum64(float v) {
   return v;                     // lane 63: the tree root
 }
 
+// The same tree for four values at once: every lane of row t (lanes
+// 16t..16t+15) returns the root of value t (a, b, c, d for t = 0..3). Levels
+// 1-4 run per value (afterwards every lane of a row holds that row's sum);
+// levels 5 and 6 exchange rows between the values with v_permlane16_swap
+// (rows [a0,a1,a2,a3], [b0..b3] -> [a0,b0,a2,b2], [a1,b1,a3,b3]) and
+// v_permlane32_swap (lane halves), so each of their adds sums the same two
+// operands as the single-value tree: (row 0 + row 1), (row 2 + row 3), then
+// (rows 0-1 + rows 2-3). Six DPP or permute adds serve four values.
+__device__ __forceinline__ float row_tree_sum16(float v) {
+  v = dpp_plus<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]  (xor 1)
+  v = dpp_plus<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]  (xor 2)
+  v = dpp_plus<0x141, 0xf>(v);  // row_half_mirror      (xor 4)
+  v = dpp_plus<0x140, 0xf>(v);  // row_mirror           (xor 8)
+  return v;
+}
+
+__device__ __forceinline__ float wave_tree_sum64x4(float a, float b, float c, float d) {
+  a = row_tree_sum16(a);
+  b = row_tree_sum16(b);
+  c = row_tree_sum16(c);
+  d = row_tree_sum16(d);
+  const auto ab = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const auto cd = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  const float sab = __uint_as_float(ab[0]) + __uint_as_float(ab[1]);  // rows: a01 b01 a23 b23
+  const float scd = __uint_as_float(cd[0]) + __uint_as_float(cd[1]);  // rows: c01 d01 c23 d23
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sab), __float_as_uint(scd), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);               // rows: a b c d
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
