@@ -33,9 +33,10 @@ all cores, at least 3 whole layers from 2048 tokens; `cpu_tok_per_s_1thread`).
 
 Kernel durations (`us_per_launch`, `gateup_us`, `down_us`) are the kernels' own:
 the stage profiler launches each stage's main kernel with events bound to its
-dispatch, the timestamps a rocprofv3 kernel trace reports. The events around
-each launch, which add the launch and cache-release gap, are kept beside them
-(`us_per_launch_events`).
+dispatch, the timestamps a rocprofv3 kernel trace reports. The events
+bracketing each stage of the eager profiled steps are only in the full
+`--report` record (`stages_us`): they also hold the host's submission gaps
+between the instrumented launches.
 """
 from __future__ import annotations
 
@@ -311,7 +312,7 @@ def dominant_roofline(r: Runner, stages):
     # reports it); the bracketing events add the launch and cache-release gap.
     kus = st.get("kernel_us_per_launch", st["us_per_launch"])
     dur_s = kus * 1e-6
-    timing = {"us_per_launch": kus, "us_per_launch_events": st["us_per_launch"],
+    timing = {"us_per_launch": kus,
               "timing": "kernel dispatch timestamps (hipExtLaunchKernelGGL events)"
               if "kernel_us_per_launch" in st else "events around the launch"}
     U = r.distinct_experts()
