@@ -149,3 +149,34 @@ def test_validate_affine_mirrors_reference_errors():
         validate_affine(q, s, s.float(), 64, 4, 3)
     with pytest.raises(ValueError, match="packed/group"):
         validate_affine(q, s[:, :, :1], s[:, :, :1], 64, 4, 3)
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (dict(rows=-1), _lib.TFM_E_INVALID, "rows"),
+    (dict(n_out=0), _lib.TFM_E_INVALID, "n_out"),
+    (dict(bits=3), _lib.TFM_E_INVALID, "bits"),
+    (dict(group=48), _lib.TFM_E_INVALID, "group_size"),
+    (dict(k_in=96), _lib.TFM_E_INVALID, "multiple of group_size"),
+    (dict(group=128), _lib.TFM_E_UNSUPPORTED, "group_size 64"),
+    (dict(dtype=7), _lib.TFM_E_INVALID, "dtype"),
+    (dict(n_out=96), _lib.TFM_E_UNSUPPORTED, "multiple of 64"),
+    (dict(x=None), _lib.TFM_E_INVALID, "x"),
+    (dict(w=None), _lib.TFM_E_INVALID, "w"),
+])
+def test_affine_qmm_rejects(args, code, msg):
+    """tfm_affine_qmm (native_affine_qmm's entry point) checks its arguments
+    before any device work: the messages of native_affine_ops.validate_affine's
+    contract and the built limits."""
+    lib = _lib.load()
+    a = dict(x=16, rows=4, w=True, n_out=128, k_in=256, group=64, bits=4, dtype=_lib.TFM_DTYPE_BF16, out=16)
+    a.update(args)
+    aff = _lib.Affine(16, 16, 16)
+    st = lib.tfm_affine_qmm(a["x"], a["rows"], ctypes.byref(aff) if a["w"] else None, a["n_out"], a["k_in"],
+                            a["group"], a["bits"], a["dtype"], a["out"], None)
+    assert st == code
+    assert msg in lib.tfm_last_error().decode()
+
+
+def test_affine_qmm_zero_rows_is_a_no_op():
+    lib = _lib.load()
+    assert lib.tfm_affine_qmm(None, 0, None, 128, 256, 64, 4, _lib.TFM_DTYPE_BF16, None, None) == _lib.TFM_OK
