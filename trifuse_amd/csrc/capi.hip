@@ -712,14 +712,18 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
     gd.slots = ws.slots;
     gd.gates_sorted = ws.gates_sorted;
     {
+      // An affine router is dequantised inside the logits kernel.
       StageScope st(TFM_STAGE_ROUTER, s);
-      const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
-      if (g.router == TFM_ROUTER_AFFINE) {
-        launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
-        rw = ws.router_w;
+      if (g.router != TFM_ROUTER_AFFINE ||
+          !launch_decode_logits_affine(f16, weights->router_bits, static_cast<const uint16_t*>(x),
+                                       weights->router_affine, weights->logit_bias, T, H, E, ws.logits, s)) {
+        const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
+        if (g.router == TFM_ROUTER_AFFINE) {
+          launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
+          rw = ws.router_w;
+        }
+        launch_decode_logits(f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T, H, E, ws.logits, s);
       }
-      launch_decode_logits(f16, static_cast<const uint16_t*>(x), rw,
-                           weights->logit_bias, T, H, E, ws.logits, s);
     }
     {
       // Top-k and grouping run in this kernel's prologue.
@@ -752,13 +756,19 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   if (gemv_decode) {
     {
       StageScope st(TFM_STAGE_ROUTER, s);
-      const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
-      if (g.router == TFM_ROUTER_AFFINE) {
-        launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
-        rw = ws.router_w;
+      if (g.router == TFM_ROUTER_AFFINE &&
+          launch_decode_logits_affine(f16, weights->router_bits, static_cast<const uint16_t*>(x),
+                                      weights->router_affine, weights->logit_bias, T, H, E, ws.logits, s)) {
+        launch_topk(g.route, f16, ws.logits, T, E, K, ws.idx, nullptr, ws.gates, s);
+      } else {
+        const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
+        if (g.router == TFM_ROUTER_AFFINE) {
+          launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
+          rw = ws.router_w;
+        }
+        launch_decode_route(g.route, f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
+                            H, E, K, ws.logits, ws.idx, ws.gates, s);
       }
-      launch_decode_route(g.route, f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
-                          H, E, K, ws.logits, ws.idx, ws.gates, s);
     }
     // The gate/up kernel publishes the grouping with its slot table and
     // sorted gates for the down GEMV.

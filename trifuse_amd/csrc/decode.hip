@@ -145,9 +145,16 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeGateUpArgs A) 
 // over E compute units (a single compute unit pulling the whole router is
 // limited by its own outstanding misses). Wave w takes tokens w, w + 4, ..,
 // two at a time.
-template <int C, bool F16>
+//
+// BITS = 0: w is the dense router [E, H] in the storage dtype. BITS = 4 or 8:
+// the router is affine-quantised (aq: codes [E, H*BITS/32] LSB first, scales
+// and biases [E, H/64] in the storage dtype) and each lane dequantises its own
+// H/64 elements in place, w = st(s*q + b) as the router dequant pass
+// computes it, so one kernel replaces that pass and its boundary.
+template <int C, bool F16, int BITS = 0>
 __global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
+                                                            tfm_affine aq,
                                                             const float* __restrict__ bias, int T,
                                                             int H, int E,
                                                             uint16_t* __restrict__ logits) {
@@ -155,14 +162,38 @@ __global__ __launch_bounds__(256) void decode_logits_kernel(const uint16_t* __re
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   float wv[C];
-  const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
+  if constexpr (BITS == 0) {
+    const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)e * H + lane * C);
 #pragma unroll
-  for (int i = 0; i < C / 8; ++i) {
-    const uint4 v = ws[i];
-    wv[8 * i + 0] = lo_st<F16>(v.x); wv[8 * i + 1] = hi_st<F16>(v.x);
-    wv[8 * i + 2] = lo_st<F16>(v.y); wv[8 * i + 3] = hi_st<F16>(v.y);
-    wv[8 * i + 4] = lo_st<F16>(v.z); wv[8 * i + 5] = hi_st<F16>(v.z);
-    wv[8 * i + 6] = lo_st<F16>(v.w); wv[8 * i + 7] = hi_st<F16>(v.w);
+    for (int i = 0; i < C / 8; ++i) {
+      const uint4 v = ws[i];
+      wv[8 * i + 0] = lo_st<F16>(v.x); wv[8 * i + 1] = hi_st<F16>(v.x);
+      wv[8 * i + 2] = lo_st<F16>(v.y); wv[8 * i + 3] = hi_st<F16>(v.y);
+      wv[8 * i + 4] = lo_st<F16>(v.z); wv[8 * i + 5] = hi_st<F16>(v.z);
+      wv[8 * i + 6] = lo_st<F16>(v.w); wv[8 * i + 7] = hi_st<F16>(v.w);
+    }
+  } else {
+    constexpr int PER = 32 / BITS;                  // codes per word
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    static_assert(C % PER == 0, "a lane's elements are whole words");
+    const int64_t k0 = (int64_t)e * H + lane * C;    // first element of this lane
+    const uint32_t* qr = static_cast<const uint32_t*>(aq.q) + k0 / PER;
+    uint32_t wd[C / PER];
+#pragma unroll
+    for (int i = 0; i < C / PER; ++i) wd[i] = qr[i];
+    // Rows are whole 64-element groups; a lane's elements span at most two.
+    const int64_t g0 = k0 / 64, g1 = (k0 + C - 1) / 64;
+    const uint16_t* sc = static_cast<const uint16_t*>(aq.scales);
+    const uint16_t* bi = static_cast<const uint16_t*>(aq.biases);
+    const float s0 = st2f<F16>(sc[g0]), b0 = st2f<F16>(bi[g0]);
+    const float s1 = st2f<F16>(sc[g1]), b1 = st2f<F16>(bi[g1]);
+    const int split = (int)((g0 + 1) * 64 - k0);     // elements j >= split are in group g1
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const float code = (float)((wd[j / PER] >> (BITS * (j % PER))) & MASK);
+      const bool second = j >= split;
+      wv[j] = st2f<F16>(f2st<F16>(__builtin_fmaf(second ? s1 : s0, code, second ? b1 : b0)));
+    }
   }
   const float be = bias ? bias[e] : 0.0f;
   // Token rows past T read zeros (offset beyond the buffer).
@@ -230,13 +261,43 @@ static int lg_for(int kin) {
 template <bool F16>
 static void decode_logits_dt(const uint16_t* x, const uint16_t* router, const float* bias, int T, int H,
                              int E, uint16_t* logits, hipStream_t s) {
+  const tfm_affine none{};
   switch (H) {
-    case 512: tfm_launch(decode_logits_kernel<8, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
-    case 1024: tfm_launch(decode_logits_kernel<16, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
-    case 1536: tfm_launch(decode_logits_kernel<24, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
-    case 2048: tfm_launch(decode_logits_kernel<32, F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
+    case 512: tfm_launch(decode_logits_kernel<8, F16>, E, 256, 0, s, x, router, none, bias, T, H, E, logits); break;
+    case 1024: tfm_launch(decode_logits_kernel<16, F16>, E, 256, 0, s, x, router, none, bias, T, H, E, logits); break;
+    case 1536: tfm_launch(decode_logits_kernel<24, F16>, E, 256, 0, s, x, router, none, bias, T, H, E, logits); break;
+    case 2048: tfm_launch(decode_logits_kernel<32, F16>, E, 256, 0, s, x, router, none, bias, T, H, E, logits); break;
     default: tfm_launch(decode_logits_generic<F16>, E, 256, 0, s, x, router, bias, T, H, E, logits); break;
   }
+}
+
+template <bool F16, int BITS>
+static bool decode_logits_affine_dt(const uint16_t* x, const tfm_affine& r, const float* bias, int T, int H,
+                                    int E, uint16_t* logits, hipStream_t s) {
+  switch (H) {
+    case 512: tfm_launch(decode_logits_kernel<8, F16, BITS>, E, 256, 0, s, x, nullptr, r, bias, T, H, E, logits); break;
+    case 1024: tfm_launch(decode_logits_kernel<16, F16, BITS>, E, 256, 0, s, x, nullptr, r, bias, T, H, E, logits); break;
+    case 1536: tfm_launch(decode_logits_kernel<24, F16, BITS>, E, 256, 0, s, x, nullptr, r, bias, T, H, E, logits); break;
+    case 2048: tfm_launch(decode_logits_kernel<32, F16, BITS>, E, 256, 0, s, x, nullptr, r, bias, T, H, E, logits); break;
+    default: return false;
+  }
+  return true;
+}
+
+bool launch_decode_logits_affine(bool f16, int bits, const uint16_t* x, const tfm_affine& router, const float* bias,
+                                 int T, int H, int E, uint16_t* logits, hipStream_t s) {
+  if (T <= 0) return true;
+  if (E > 64) fail(TFM_E_UNSUPPORTED, "decode routing: more than 64 experts");
+  if (!logits) fail(TFM_E_INVALID, "decode routing: logits buffer missing");
+  bool ok;
+  if (f16)
+    ok = bits == 8 ? decode_logits_affine_dt<true, 8>(x, router, bias, T, H, E, logits, s)
+                   : decode_logits_affine_dt<true, 4>(x, router, bias, T, H, E, logits, s);
+  else
+    ok = bits == 8 ? decode_logits_affine_dt<false, 8>(x, router, bias, T, H, E, logits, s)
+                   : decode_logits_affine_dt<false, 4>(x, router, bias, T, H, E, logits, s);
+  if (ok) check_hip(hipGetLastError(), "decode logits launch");
+  return ok;
 }
 
 void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, const float* bias, int T,

@@ -139,6 +139,11 @@ void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, i
 void launch_decode_route(int route_kind, bool f16, const uint16_t* x, const uint16_t* router, const float* bias,
                          int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
                          hipStream_t s);
+// The decode logits on the affine router itself (bits 4 or 8), each row
+// dequantised in the kernel as the dequant pass would round it; false (nothing
+// launched) for a hidden size without a variant.
+bool launch_decode_logits_affine(bool f16, int bits, const uint16_t* x, const tfm_affine& router, const float* bias,
+                                 int T, int H, int E, uint16_t* logits, hipStream_t s);
 void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, const float* bias, int T,
                           int H, int E, uint16_t* logits, hipStream_t s);
 
