@@ -319,16 +319,17 @@ def dominant_roofline(r: Runner, stages):
     H, I = g.hidden, g.intermediate
     gu_bytes_expert = 2 * (I * H * r.wl.bits // 8 + 2 * (I * H // 64) * 2)
     R = T * g.top_k
-    # The library's decode path choice: the decode GEMV kernels (4-bit codes,
-    # bf16 or half storage) up to 176 routes from 4 tokens; the streaming
-    # kernels (every storage dtype and code width) at 1 to 3 tokens and for
-    # batches the GEMV kernels do not run, while the token rows fit their
-    # prologue; else the grouped GEMM.
-    gemv = R <= 176 and r.wl.bits == 4
+    # The library's decode path choice: the streaming kernels at 1 to 3
+    # tokens while the token rows fit their prologue, and for 8-bit codes
+    # wherever they fit; the decode GEMV kernels (4-bit codes, bf16 or half
+    # storage) from 4 tokens up to E + 40 routes (at most 176); else the
+    # grouped GEMM.
+    gemv = R <= min(176, g.experts + 40) and r.wl.bits == 4
     fits = (R <= 256 and g.experts <= 64 and T * (H // 32) <= 1024 and
             T * (H // 32) * 68 + R * 4 <= 65536 and  # staged x rows in LDS
             H % 512 == 0 and 512 <= H <= 2048 and I % 512 == 0 and 512 <= I <= 2048)
-    streaming = fits and (T <= 3 or not gemv)
+    streaming = fits and (T <= 3 or r.wl.bits != 4)
+    gemv = gemv and not (fits and T <= 3)
     # 4-bit weights with inputs up to 2048 wide (a multiple of 128) run the
     # weights-in-registers grouped GEMM, everything else the LDS-dequant one
     wr = r.wl.bits == 4 and H <= 2048 and H % 128 == 0

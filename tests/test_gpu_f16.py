@@ -59,7 +59,7 @@ def _check(geom, T, bits=4, dtype=F16, rm=1.0, tag="f16", layer_id=0, router_bit
     return blk, layer, x
 
 
-# 1-3 tokens: streaming kernels; 4 up to 176 routes (OLMoE 22 tokens):
+# 1-3 tokens: streaming kernels; 4 up to E + 40 routes (OLMoE 13 tokens):
 # decode GEMV kernels; beyond: grouped GEMM.
 @pytest.mark.parametrize("geom_name,T", [("olmoe", 1), ("olmoe", 4), ("olmoe", 8), ("olmoe", 22),
                                          ("olmoe", 23), ("olmoe", 512), ("granite", 1), ("granite", 5),

@@ -239,6 +239,50 @@ static bool fused_decode(const tfm_geometry& g, int64_t R) {
   return R <= 256 && g.hidden_size <= 2048 && g.intermediate_size <= 2048;
 }
 
+// Decode path override for measurement, read once (TFM_DECODE_PATH): 1
+// streaming kernels (where they fit), 2 decode GEMV kernels (4-bit codes,
+// whatever the route count), 3 grouped GEMM; 0 (unset) the automatic choice.
+static int decode_path_override() {
+  static const int v = [] {
+    const char* s = std::getenv("TFM_DECODE_PATH");
+    if (!s) return 0;
+    if (!std::strcmp(s, "stream")) return 1;
+    if (!std::strcmp(s, "gemv")) return 2;
+    if (!std::strcmp(s, "gemm")) return 3;
+    std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_DECODE_PATH=%s\n", s);
+    return 0;
+  }();
+  return v;
+}
+
+// The decode path of a block: streaming kernels, decode GEMV kernels or (both
+// false) the grouped GEMM.
+struct DecodeChoice {
+  bool stream, gemv;
+};
+static DecodeChoice decode_choice(const tfm_geometry& g, int64_t R, int gemv_max_routes) {
+  const int T = (int)(R / g.experts_per_token);
+  const bool fused = fused_decode(g, R);
+  const bool fits = fused && decode_stream_fits(T, g.experts_per_token, g.num_experts, g.hidden_size,
+                                                g.intermediate_size);
+  const bool gemv_ok = fused && g.bits == 4;  // the GEMV kernels take 4-bit codes
+  switch (decode_path_override()) {
+    case 1: if (fits) return {true, false}; break;
+    case 2: if (gemv_ok) return {false, true}; break;
+    case 3: return {false, false};
+    default: break;
+  }
+  // 4-bit codes: streaming kernels up to ds_max_tokens(), then the GEMV
+  // kernels, then the grouped GEMM (faster than the streaming kernels there:
+  // OLMoE 14 tokens 70.5 against 83.6 us, Granite 16 tokens 37.2 against
+  // 50.7). 8-bit codes, which no GEMV kernel runs: streaming wherever the
+  // token rows fit (8 tokens: 84 against 140 us on the grouped GEMM).
+  const bool stream_small = fits && T <= ds_max_tokens();
+  const bool gemv = gemv_ok && !stream_small && R <= gemv_max_routes;
+  return {stream_small || (fits && !gemv_ok), gemv};
+}
+
+
 struct GroupWs {
   WsHeader* hdr;
   Grouping grp;
@@ -283,28 +327,41 @@ static void check_affine(const tfm_affine& a, const char* name) {
 }
 
 // Routes up to which expert products run the GEMV kernels (decode.hip,
-// gemv.hip) instead of the grouped GEMM, on every entry point: the forward
-// path's decode GEMV, the hook path and tfm_gather_qmm, so that all of them
-// run the same kernels on the same routes. Past about 176 routes (OLMoE 22
-// tokens) the GEMM's 64-row tiles are faster: OLMoE measured 81.2 and 86.3 us
-// per layer at 20 and 22 tokens on the GEMV kernels (96.4 and 87.7 on the
-// GEMM), 88.7 and 90.9 at 23 and 24 (88.4 and 88.5 on the GEMM); Granite 50.5
-// and 52.3 at 22 and 23 tokens (50.7 and 50.9); Granite decode 32 65.4 on the
-// GEMV kernels against 51.6. TFM_GEMV_MAX_ROUTES overrides (an integer in
-// [0, 2^30]; anything else is reported and ignored).
-static int gemv_threshold() {
+// gemv.hip) instead of the grouped GEMM. TFM_GEMV_MAX_ROUTES (an integer in
+// [0, 2^30]) sets it for every entry point; -1 when unset.
+static int gemv_threshold_env() {
   static int v = [] {
     const char* s = std::getenv("TFM_GEMV_MAX_ROUTES");
-    if (!s) return 176;
+    if (!s) return -1;
     char* end = nullptr;
     const long n = std::strtol(s, &end, 10);
     if (!end || end == s || *end != 0 || n < 0 || n > (1 << 30)) {
       std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_GEMV_MAX_ROUTES=%s\n", s);
-      return 176;
+      return -1;
     }
     return (int)n;
   }();
   return v;
+}
+
+// tfm_gather_qmm and tfm_affine_qmm without a plan: 176 routes.
+static int gemv_threshold() {
+  const int v = gemv_threshold_env();
+  return v >= 0 ? v : 176;
+}
+
+// The MoE block (forward, hook and GPUCallable paths alike, so that they run
+// the same kernels on the same routes): E + 40 routes, at most 176. Since the
+// grouped GEMM's four-wave 64-row tiles the GEMM wins from a little under two
+// routes per expert. Per layer, decode GEMV against grouped GEMM: OLMoE 12
+// tokens (96 routes) 63.8 against 69.2 us, 13 tokens 67.5 against 70.2, 14
+// tokens 70.7 against 70.5, 16 tokens 74.6 against 71.5, 20 tokens 82.9
+// against 73.1; Granite 10 tokens (80 routes) 36.1 against 36.8, 11 tokens
+// 37.6 against 36.9, 16 tokens 43.7 against 37.2, 20 tokens 49.7 against
+// 38.0, decode 32 63.3 against 39.2.
+static int block_gemv_threshold(int E) {
+  const int v = gemv_threshold_env();
+  return v >= 0 ? v : std::min(176, E + 40);
 }
 
 // Expert part of the block on grouped routes (flat routes t*K+k of idx).
@@ -317,12 +374,12 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
   const int H = g.hidden_size, I = g.intermediate_size, E = g.num_experts, K = g.experts_per_token;
   const int64_t R = T * K;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
-  const bool small = R <= p->gemv_max_routes && H <= 2048 && I <= 2048;
-  // The standalone GEMV kernels (gemv.hip) take 4-bit codes (bf16 or half storage).
-  const bool gemv = small && g.bits == 4;
-  // The streaming kernels at the sizes where tfm_moe_forward runs them.
-  if (!grouped && fused_decode(g, R) && decode_stream_fits((int)T, K, E, H, I) &&
-      ((int)T <= ds_max_tokens() || !gemv)) {
+  // The path tfm_moe_forward takes for these routes, so that both entry
+  // points run the same kernels (the GEMV kernels take 4-bit codes, bf16 or
+  // half storage).
+  const DecodeChoice dc = decode_choice(g, R, p->gemv_max_routes);
+  const bool gemv = dc.gemv && H <= 2048 && I <= 2048;
+  if (!grouped && dc.stream) {
     // Streaming decode kernels, the same ones tfm_moe_forward runs at decode
     // shapes, so both entry points give bit-identical results.
     Grouping gd = ws.grp;
@@ -446,7 +503,7 @@ int tfm_plan_create(const tfm_geometry* geometry, tfm_plan** plan_out) {
     tfm_plan* p = new tfm_plan{};
     p->g = *geometry;
     p->device = dev;
-    p->gemv_max_routes = gemv_threshold();
+    p->gemv_max_routes = block_gemv_threshold(geometry->num_experts);
     p->scratch = scr;
     p->scratch_error = why;
     *plan_out = p;
@@ -706,8 +763,9 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
   const int T = (int)tokens, E = g.num_experts, K = g.experts_per_token;
   const int H = g.hidden_size, I = g.intermediate_size;
   const bool f16 = g.dtype == TFM_DTYPE_F16;
-  const bool gemv_decode = fused_decode(g, R) && R <= plan->gemv_max_routes && g.bits == 4;
-  if (fused_decode(g, R) && decode_stream_fits(T, K, E, H, I) && (T <= ds_max_tokens() || !gemv_decode)) {
+  const DecodeChoice dc = decode_choice(g, R, plan->gemv_max_routes);
+  const bool gemv_decode = dc.gemv;
+  if (dc.stream) {
     Grouping gd = ws.grp;
     gd.slots = ws.slots;
     gd.gates_sorted = ws.gates_sorted;
