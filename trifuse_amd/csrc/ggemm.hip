@@ -56,7 +56,11 @@ struct GgArgs {
   int N;                 // output columns of one matrix
   int Kin;
   uint16_t* out;         // gate/up: h [n_routes, N]; down: y [n_routes, N]; plain: out [rows, N]
+  int sb_layout;         // ggemm_wr_kernel's scale/bias layout in LDS (kSbPlain, kSbDword, kSbChunk)
 };
+
+// Scale/bias layouts of ggemm_wr_kernel's LDS copy (see there).
+enum { kSbPlain = 0, kSbDword = 1, kSbChunk = 2 };
 
 // Row of accumulator element v of lane `lane` inside a 32x32 block of
 // v_mfma_f32_32x32x16_bf16 (its column is lane % 32; operands: lane l
@@ -121,6 +125,15 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* ds
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
 #else
   (void)r; (void)dst; (void)voff; (void)soff;
+#endif
+}
+
+// The same with 4 bytes per lane: lane l's dword lands at dst + 4 l bytes.
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, 0, 0, 0);
+#else
+  (void)r; (void)dst; (void)voff;
 #endif
 }
 
@@ -696,10 +709,27 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
       raw[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(live ? rbq[j] : rnull, b_qoff[j], kt * 64, 0));
   };
 
-  // Scales and biases of the tile's rows, copied once (as in ggemm_kernel's
-  // SL path): HALVES contiguous row ranges, each at a 1 KB-aligned offset.
+  // Scales and biases of the tile's rows, copied once: HALVES contiguous row
+  // ranges, each at a 1 KB-aligned offset, row r of a range at r * 2G bytes.
+  // sb_read reads one group of 16 consecutive rows per instruction; at a row
+  // stride of 2G bytes those rows share 2 to 4 banks (32 or 64 banks of 4
+  // bytes). The layouts move row r's group-pair dword d to d ^ sw(r):
+  //  * kSbPlain: sw = 0, copied as contiguous 16-byte pieces;
+  //  * kSbDword: sw(r) = (r G / 64) mod (G/2) for G/2 a power of two, which
+  //    puts the 16 rows in 16 banks; copied with 4-byte LDS-DMA, the swizzle
+  //    applied to the source offsets;
+  //  * kSbChunk (G = 16 or 32): 16-byte pieces of a row swapped,
+  //    sw(r) = 4 ((r / 4) mod (G/8)): 2 rows per bank at worst, and the copy
+  //    stays 16-byte LDS-DMA.
   constexpr int HALVES = MODE == kGgGateUp ? 2 : 1;
   constexpr int HROWS = BN / HALVES;
+  const int GH = G / 2;                           // group-pair dwords per row
+  const int CH = G / 8;                           // 16-byte pieces per row
+  const int lay = args.sb_layout;
+  const int swm = (GH & (GH - 1)) == 0 ? GH - 1 : 0;
+  auto sb_swz = [&](int r) {
+    return lay == kSbDword ? ((r * G) >> 6) & swm : lay == kSbChunk ? ((r >> 2) & (CH - 1)) << 2 : 0;
+  };
   const int hbytes = HROWS * G * 2;
   const int hs = (hbytes + 1023) & ~1023;
 #pragma unroll
@@ -709,22 +739,42 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
     const auto rs = gg_rsrc(static_cast<const char*>(bm.scales) + ebase * srow, (uint32_t)args.N * srow);
     const auto rb = gg_rsrc(static_cast<const char*>(bm.biases) + ebase * srow, (uint32_t)args.N * srow);
     const uint32_t g0 = (uint32_t)n0 * srow;
-    for (int c = wave; c * 1024 < hbytes; c += WAVES) {
-      lds_dma16(rs, sSc + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
-      lds_dma16(rb, sBi + (h * hs + c * 1024) / 2, g0 + c * 1024 + lane * 16, 0);
+    if (lay == kSbDword) {
+      for (int c = wave; c * 256 < hbytes; c += WAVES) {
+        const int p = 64 * c + lane;              // destination dword of the range
+        const int r = p / GH, x = p - r * GH;
+        const uint32_t src = 4 * p < hbytes ? g0 + (uint32_t)r * srow + 4u * (uint32_t)(x ^ sb_swz(r)) : kOob;
+        lds_dma4(rs, sSc + (h * hs + c * 256) / 2, src);
+        lds_dma4(rb, sBi + (h * hs + c * 256) / 2, src);
+      }
+    } else {
+      for (int c = wave; c * 1024 < hbytes; c += WAVES) {
+        uint32_t src = g0 + c * 1024 + lane * 16;
+        if (lay == kSbChunk) {
+          const int p = 64 * c + lane;            // destination 16-byte piece of the range
+          const int r = p / CH, x = p - r * CH;
+          src = 16 * p < hbytes ? g0 + (uint32_t)r * srow + 16u * (uint32_t)(x ^ (sb_swz(r) >> 2)) : kOob;
+        }
+        lds_dma16(rs, sSc + (h * hs + c * 1024) / 2, src, 0);
+        lds_dma16(rb, sBi + (h * hs + c * 1024) / 2, src, 0);
+      }
     }
   }
-  int sidx[2];
+  int sidx[2], ssw[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) sidx[j] = (trow[j] / HROWS) * (hs / 2) + (trow[j] % HROWS) * G;
+  for (int j = 0; j < 2; ++j) {
+    sidx[j] = (trow[j] / HROWS) * (hs / 2) + (trow[j] % HROWS) * G;
+    ssw[j] = sb_swz(trow[j] % HROWS);
+  }
   // scale and bias of super-step kt for both rows (past the end: last group)
   auto sb_read = [&](float* sc, float* bi, int kt) {
     int g = 2 * kt + (g4 >> 1);
     g = g < G ? g : G - 1;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      sc[j] = st2f<F16>(sSc[sidx[j] + g]);
-      bi[j] = st2f<F16>(sBi[sidx[j] + g]);
+      const int o = sidx[j] + 2 * ((g >> 1) ^ ssw[j]) + (g & 1);
+      sc[j] = st2f<F16>(sSc[o]);
+      bi[j] = st2f<F16>(sBi[o]);
     }
   };
   auto deq = [&](op_t* b, const uint4* raw, const float* sc, const float* bi, int s) {
@@ -1035,8 +1085,26 @@ static int wr_waves(int64_t tiles8) {
   return tiles8 < 2 * (int64_t)gg_device_cus() ? 4 : 8;
 }
 
+// Scale/bias layout of ggemm_wr_kernel for an input width (TFM_GGEMM_SB_LAYOUT
+// = 0/1/2 forces kSbPlain/kSbDword/kSbChunk where it applies): kSbChunk at
+// 16 and 32 groups per row, else kSbPlain. Per layer, plain / dword / chunk
+// layouts on one box: OLMoE 4096 tokens (Zipf) 517.7 / 512.5 / 509.8 us
+// (gate/up 274.2 / 268.9 / 267.0), 512 tokens 138.1 / 135.5 / 134.9; Granite
+// 2048 tokens 156.5 / 157.4 / 156.3, decode 32 39.7 / 40.3 / 39.7.
+static int sb_layout(int Kin) {
+  static const int o = [] {
+    const char* s = std::getenv("TFM_GGEMM_SB_LAYOUT");
+    return s ? std::atoi(s) : -1;
+  }();
+  const int G = Kin / BK;
+  if (o == kSbPlain || o == kSbDword) return o;
+  return G == 16 || G == 32 ? kSbChunk : kSbPlain;
+}
+
 template <int BM, int MODE, bool F16, int WV>
-static void launch_wr_waves(const GgArgs& a, int64_t n_routes, int E, hipStream_t s) {
+static void launch_wr_waves(const GgArgs& a_in, int64_t n_routes, int E, hipStream_t s) {
+  GgArgs a = a_in;
+  a.sb_layout = sb_layout(a.Kin);
   constexpr int OUT_COLS = MODE == kGgGateUp ? 16 * WV : 32 * WV;
   const int NT = (a.N + OUT_COLS - 1) / OUT_COLS;
   // With 256-row tiles an XCD's run of cheap tiles holds more tiles than an
