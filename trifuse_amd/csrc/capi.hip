@@ -212,6 +212,20 @@ static int ds_max_tokens() {
   return v;
 }
 
+// Whether the one- and two-token gate/up kernel also copies the routed
+// experts' down weights toward the down + combine kernel (TFM_DS_PREFETCH=1;
+// off by default). Off measured faster once both kernels issued their loads
+// early: per layer on one box, with against without, OLMoE 1 token 16.94
+// against 16.83 us, 2 tokens 26.9 against 24.9; Granite 1 token 12.87
+// against 12.39.
+static bool ds_prefetch() {
+  static const bool v = [] {
+    const char* s = std::getenv("TFM_DS_PREFETCH");
+    return s != nullptr && std::strcmp(s, "1") == 0;
+  }();
+  return v;
+}
+
 // Tokens up to which the prefill-path routing runs as two kernels (router
 // logits with one wave per few (token, expert) pairs, then top-k with the
 // chunk histograms) rather than the fused router + top-k kernel, whose
@@ -787,7 +801,8 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
       // Top-k and grouping run in this kernel's prologue.
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_ds_gateup(f16, g.bits, g.route, static_cast<const uint16_t*>(x), ws.logits, ws.idx, ws.gates, T, K, E, H,
-                       I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s, &weights->down);
+                       I, weights->gate, weights->up, gd, &ws.hdr->status, ws.h, s,
+                       ds_prefetch() ? &weights->down : nullptr);
     }
     const int max_active = (int)(R < E ? R : E);
     if (decode_small(T, K)) {
