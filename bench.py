@@ -337,12 +337,12 @@ def dominant_roofline(r: Runner, stages):
     if is_decode(r.wl):
         # Per launch: routed experts' gate+up Q/S/B, x rows in, h rows out.
         per_launch = sum(u * gu_bytes_expert + T * H * 2 + T * g.top_k * I * 2 for u in U) / len(U)
-        # With TFM_DS_PREFETCH=1 the one- and two-token gate/up kernel (T*K
-        # <= 16) also copies the routed experts' down Q/S/B from HBM for the
+        # With TFM_DS_PREFETCH=1 the gate/up kernel of 1 to 3 tokens (T*K
+        # <= 24) also copies the routed experts' down Q/S/B from HBM for the
         # fused down+combine kernel: those bytes are then moved by this kernel.
         dn_bytes_expert = H * I * r.wl.bits // 8 + 2 * (H * I // 64) * 2
         pf_on = os.environ.get("TFM_DS_PREFETCH") == "1"
-        prefetch = (sum(U) / len(U) * dn_bytes_expert) if (pf_on and streaming and T <= 2 and R <= 16) else 0.0
+        prefetch = (sum(U) / len(U) * dn_bytes_expert) if (pf_on and streaming and T <= 3 and R <= 24) else 0.0
         achieved = (per_launch + prefetch) / dur_s / 1e9
         label = "ds_gateup_kernel" if streaming else "decode_gateup_kernel" if gemv else gemm_label
         return {"kernel": label,

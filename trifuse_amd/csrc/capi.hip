@@ -193,10 +193,10 @@ static BlockWs carve_block(const tfm_geometry& g, int64_t T, void* base) {
 // 2 tokens 26.4 against 29.6, 3 tokens 35.5 against 34.6, 8 tokens (16
 // layers) 56.0 against 53.0, 12 tokens 75.6 against 63.2; Granite 1 token
 // 12.6 against 18.0, 2 tokens 17.6 against 21.1, 3 tokens 23.9 against 23.9,
-// 8 tokens 34.9 against 32.5. The one- and two-token streaming layer is three
-// kernels (the down projection fused with the combine); 3 tokens stay on the
-// streaming kernels too (0.9 us slower for OLMoE, level for Granite), so that
-// the smallest batches give the same bits as the general streaming layer.
+// 8 tokens 34.9 against 32.5. The streaming layer of 1 to 3 tokens is three
+// kernels (the down projection fused with the combine): 3 tokens went from
+// 35.3 to 32.2 us (OLMoE) and from 24.4 to 21.6 (Granite) with it, against
+// 34.6 and 23.9 on the GEMV kernels.
 static int ds_max_tokens() {
   static const int v = [] {
     const char* s = std::getenv("TFM_DS_MAX_TOKENS");
@@ -212,7 +212,7 @@ static int ds_max_tokens() {
   return v;
 }
 
-// Whether the one- and two-token gate/up kernel also copies the routed
+// Whether the gate/up kernel of 1 to 3 tokens also copies the routed
 // experts' down weights toward the down + combine kernel (TFM_DS_PREFETCH=1;
 // off by default). Off measured faster once both kernels issued their loads
 // early: per layer on one box, with against without, OLMoE 1 token 16.94

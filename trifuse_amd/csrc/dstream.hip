@@ -391,8 +391,9 @@ struct DsGateUpArgs {
   Grouping grp;            // published by workgroup 0, with slots and gates_sorted
   uint32_t* status;
   uint16_t* h;  // [R, I]
-  // Down weights to prefetch for ds_down_combine_kernel (q null: none). Its
-  // workgroup b reads rows 4b..4b+3 of every routed expert.
+  // Down weights to prefetch for ds_down_combine_kernel (q null: none, the
+  // default; the caller passes them only on request). Its workgroup b reads
+  // rows 4b..4b+3 of every routed expert.
   tfm_affine pf;
 };
 
@@ -585,7 +586,9 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     ds_load_row<C>(ds_mat(A.up, e, N, H), n, H, ll, w.u);
   };
 
-  // Down-weight prefetch. When the down projection runs as
+  // Down-weight prefetch (only when the caller asks for it: reading the down
+  // weights from HBM in the down kernel measured faster once that kernel
+  // issued its loads right after the route ids). When the down projection runs as
   // ds_down_combine_kernel, its workgroup b' reads rows 4b'..4b'+3 of every
   // routed expert's down matrix: packed codes, scales and biases, three
   // contiguous runs. Workgroup b of this kernel copies them for b' = b,
@@ -856,13 +859,17 @@ struct DsDownCombineArgs {
 };
 
 // NT threads: NT/64 waves share the routes (route f to wave f mod NT/64).
-template <int C, int NT>
+// Instances: at most TMAX tokens and RMAX routes, FW = RMAX / (NT/64) routes
+// per wave. Batches of up to 2 tokens and 16 routes run the instance sized
+// for them: the one sized for 3 tokens made the one-token layer 5% slower.
+template <int C, int NT, int RMAX, int TMAX>
 __global__ __launch_bounds__(NT) void ds_down_combine_kernel(DsDownCombineArgs A) {
   extern __shared__ uint4 ds_lds[];
-  __shared__ float s_p[kDsSmallR][4];  // product of route f for row 4*blockIdx.x + r
+  __shared__ float s_p[RMAX][4];  // product of route f for row 4*blockIdx.x + r
   constexpr int nch = 16 * C;
   constexpr int NW = NT / 64;
-  constexpr int FW = (kDsSmallR + NW - 1) / NW;  // routes per wave
+  constexpr int FW = (RMAX + NW - 1) / NW;  // routes per wave
+  static_assert(RMAX <= kDsSmallR && TMAX <= kDsSmallT, "within the small-batch limits");
   const int T = A.T, K = A.K, E = A.E, N = A.H, kin = A.I;
   const int R = T * K;
   uint4* xs = ds_lds;                                        // [R][4][nch]
@@ -900,10 +907,10 @@ __global__ __launch_bounds__(NT) void ds_down_combine_kernel(DsDownCombineArgs A
   // that the final sum does not wait for it.
   // Kept as storage bits until the sum: converted here, they would make the
   // wave wait for every load issued so far.
-  uint32_t res[kDsSmallT] = {};
+  uint32_t res[TMAX] = {};
   if (wave == 0 && ll == 0 && n < N && A.residual) {
 #pragma unroll
-    for (int t = 0; t < kDsSmallT; ++t)
+    for (int t = 0; t < TMAX; ++t)
       if (t < T) res[t] = A.residual[(int64_t)t * N + n];
   }
   // This wave's routes' weight rows, then every route's h row (sorted
@@ -948,7 +955,7 @@ __global__ __launch_bounds__(NT) void ds_down_combine_kernel(DsDownCombineArgs A
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int t = 0; t < kDsSmallT; ++t) {
+    for (int t = 0; t < TMAX; ++t) {
       if (t >= T) break;
       // Bad routes hold a product of +0, and the sum (from +0) is never -0,
       // so adding them changes no bit: the K reads go out together.
@@ -1079,11 +1086,12 @@ void launch_ds_gateup(int mode, const uint16_t* x, const uint16_t* logits, int32
   const int pipe = env_int("TFM_DS_PIPE", 1, 1, 2);
   const int per = T * (H / 32);
   const int xch = per <= nt ? 1 : per <= 2 * nt ? 2 : 4;
-  // At one token a copy wave issues the down-weight copies; at two the
-  // compute waves do, before their items (TFM_DS_COPY_WAVE=0/1 forces either;
-  // without the copy wave, one token's copies follow the items). Per layer:
-  // OLMoE 1 token 16.75 us with the copy wave, 17.36 without; 2 tokens 30.8
-  // with, 26.4 without; Granite 2 tokens 17.8 either way.
+  // With down-weight copies requested: at one token a copy wave issues them;
+  // at two the compute waves do, before their items (TFM_DS_COPY_WAVE=0/1
+  // forces either; without the copy wave, one token's copies follow the
+  // items). Per layer, copies on: OLMoE 1 token 16.75 us with the copy wave,
+  // 17.36 without; 2 tokens 30.8 with, 26.4 without; Granite 2 tokens 17.8
+  // either way.
   const bool copy_wave = A.pf.q != nullptr && env_int("TFM_DS_COPY_WAVE", T == 1 ? 1 : 0, 0, 1) == 1;
 #define TFM_DS_GU_P(CV, XV, NV, PV, MV)                                                              \
   if (copy_wave && XV == 1 && NV == 256 && PV == 1) {                                              \
@@ -1200,13 +1208,17 @@ void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t
   const unsigned grid = (unsigned)((H + 3) / 4);
   // Eight waves (one route each at one token) unless TFM_DS_DC_THREADS=256.
   const int nt = env_int("TFM_DS_DC_THREADS", 512, 256, 512) >= 512 ? 512 : 256;
-#define TFM_DS_DC(CV)                                     \
-  if (nt == 512) {                                        \
-    allow_lds(ds_down_combine_kernel<CV, 512>, lds);      \
-    tfm_launch(ds_down_combine_kernel<CV, 512>, grid, 512, lds, s, A); \
-  } else {                                                \
-    allow_lds(ds_down_combine_kernel<CV, 256>, lds);      \
-    tfm_launch(ds_down_combine_kernel<CV, 256>, grid, 256, lds, s, A); \
+  const bool two = T <= 2 && R <= 16;  // the instance for at most 2 tokens and 16 routes
+#define TFM_DS_DC_F(CV, NV, RV, TV)                                     \
+  {                                                                     \
+    allow_lds(ds_down_combine_kernel<CV, NV, RV, TV>, lds);             \
+    tfm_launch(ds_down_combine_kernel<CV, NV, RV, TV>, grid, NV, lds, s, A); \
+  }
+#define TFM_DS_DC(CV)                                                                             \
+  if (nt == 512) {                                                                                \
+    if (two) TFM_DS_DC_F(CV, 512, 16, 2) else TFM_DS_DC_F(CV, 512, kDsSmallR, kDsSmallT)         \
+  } else {                                                                                        \
+    if (two) TFM_DS_DC_F(CV, 256, 16, 2) else TFM_DS_DC_F(CV, 256, kDsSmallR, kDsSmallT)         \
   }
   switch (I / 512) {
     case 1: TFM_DS_DC(1) break;
@@ -1216,6 +1228,7 @@ void launch_ds_down_combine(const uint16_t* h, bool h_route_order, const int32_t
     default: fail(TFM_E_UNSUPPORTED, "decode down+combine: intermediate width");
   }
 #undef TFM_DS_DC
+#undef TFM_DS_DC_F
   check_hip(hipGetLastError(), "decode down+combine launch");
 }
 

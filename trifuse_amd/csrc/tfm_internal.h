@@ -161,8 +161,8 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
 constexpr int kDsGivenRoutes = 2;
 // Small batches whose down projection runs fused with the combine
 // (decode_small): at most kDsSmallT tokens and kDsSmallR routes.
-constexpr int kDsSmallT = 2;
-constexpr int kDsSmallR = 16;
+constexpr int kDsSmallT = 3;
+constexpr int kDsSmallR = 24;
 // Row order of the gate/up kernel's h output: route order (h row f = flat
 // route f) for one token with ranked routes whose down projection is the
 // fused down + combine kernel (K <= kDsSmallR); expert-sorted order
