@@ -13,8 +13,11 @@ from trifuse_amd import workload as wl
 # (geometry, tokens): one and two tokens take the streaming decode kernels
 # (the down-weight copies when TFM_DS_PREFETCH=1); 300 OLMoE tokens and 64
 # Granite tokens take the grouped GEMM at 32, 16 and 8 quantisation groups
-# per row (the scale/bias layouts of TFM_GGEMM_SB_LAYOUT).
-CASES = [("olmoe", 1), ("olmoe", 2), ("granite", 1), ("olmoe", 300), ("granite", 64)]
+# per row (the scale/bias layouts of TFM_GGEMM_SB_LAYOUT); 8 tokens take the
+# decode GEMV kernels (OLMoE with the published slot table, Granite with the
+# grouping in every gate/up workgroup: TFM_DECODE_GROUPING swaps them).
+CASES = [("olmoe", 1), ("olmoe", 2), ("granite", 1), ("olmoe", 300), ("granite", 64), ("olmoe", 8),
+         ("granite", 8)]
 
 
 def outputs(device="cuda:0"):

@@ -1,7 +1,8 @@
 """Tuning overrides that change how the kernels move data but not what they
-compute give the same bits as the defaults: the one- and two-token
-down-weight copies (TFM_DS_PREFETCH=1) and the grouped GEMM's plain and
-dword-swizzled scale/bias layouts in LDS (TFM_GGEMM_SB_LAYOUT=0/1). The
+compute give the same bits as the defaults: the down-weight copies of 1 to
+3 tokens (TFM_DS_PREFETCH=1), the grouped GEMM's plain and dword-swizzled
+scale/bias layouts in LDS (TFM_GGEMM_SB_LAYOUT=0/1) and either grouping of
+the decode GEMV path (TFM_DECODE_GROUPING=slots/workgroup). The
 overrides are read once per process, so each runs in a child process."""
 import os
 import subprocess
@@ -24,7 +25,9 @@ def default_outputs(gpu):
 
 
 @pytest.mark.parametrize("env", [{"TFM_DS_PREFETCH": "1"}, {"TFM_GGEMM_SB_LAYOUT": "0"},
-                                 {"TFM_GGEMM_SB_LAYOUT": "1"}], ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
+                                 {"TFM_GGEMM_SB_LAYOUT": "1"}, {"TFM_DECODE_GROUPING": "slots"},
+                                 {"TFM_DECODE_GROUPING": "workgroup"}],
+                         ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
 def test_override_gives_default_bits(default_outputs, env, tmp_path):
     log(f"override {env}")
     path = tmp_path / "out.npz"

@@ -212,6 +212,30 @@ static int ds_max_tokens() {
   return v;
 }
 
+// Grouping of the decode GEMV path (TFM_DECODE_GROUPING=slots|workgroup
+// forces one). With many gate/up workgroups (at least 4096: OLMoE from 4
+// tokens), one route-and-group workgroup publishes the slot table after the
+// logits and every gate/up workgroup reads its slot (gemv_kernel); with few
+// (Granite), the multi-workgroup top-k runs instead and every gate/up
+// workgroup groups the routes itself (decode_gateup_kernel): the single
+// workgroup costs about 1.9 us more than the top-k, and each gate/up
+// workgroup saves about 0.7 us of grouping. Per layer, slots against
+// in-workgroup grouping, one box: OLMoE 4 tokens 39.3 against 39.4 us,
+// 8 tokens (16 layers) 53.6 against 55.5, 12 tokens 64.1 against 65.4;
+// Granite 4 tokens 27.8 against 26.3, 8 tokens 34.2 against 33.2.
+static bool decode_slot_grouping(int T, int K, int E, int H, int I) {
+  static const int o = [] {
+    const char* s = std::getenv("TFM_DECODE_GROUPING");
+    if (!s) return -1;
+    if (!std::strcmp(s, "slots")) return 1;
+    if (!std::strcmp(s, "workgroup")) return 0;
+    std::fprintf(stderr, "trifuse_moe: ignoring invalid TFM_DECODE_GROUPING=%s\n", s);
+    return -1;
+  }();
+  if (o >= 0) return o == 1;
+  return decode_gateup_workgroups(T, K, E, H, I) >= 4096;
+}
+
 // Whether the gate/up kernel of 1 to 3 tokens also copies the routed
 // experts' down weights toward the down + combine kernel (TFM_DS_PREFETCH=1;
 // off by default). Off measured faster once both kernels issued their loads
@@ -832,23 +856,37 @@ static void moe_forward_body(const tfm_plan* plan, const void* x, int64_t tokens
       if (g.router == TFM_ROUTER_AFFINE &&
           launch_decode_logits_affine(f16, weights->router_bits, static_cast<const uint16_t*>(x),
                                       weights->router_affine, weights->logit_bias, T, H, E, ws.logits, s)) {
-        launch_topk(g.route, f16, ws.logits, T, E, K, ws.idx, nullptr, ws.gates, s);
+        // An affine router is dequantised inside the logits kernel.
       } else {
         const uint16_t* rw = static_cast<const uint16_t*>(weights->router);
         if (g.router == TFM_ROUTER_AFFINE) {
           launch_dequant_router(f16, weights->router_bits, weights->router_affine, E, H, ws.router_w, s);
           rw = ws.router_w;
         }
-        launch_decode_route(g.route, f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T,
-                            H, E, K, ws.logits, ws.idx, ws.gates, s);
+        launch_decode_logits(f16, static_cast<const uint16_t*>(x), rw, weights->logit_bias, T, H, E, ws.logits, s);
       }
     }
-    // The gate/up kernel publishes the grouping with its slot table and
-    // sorted gates for the down GEMV.
     Grouping gd = ws.grp;
     gd.slots = ws.slots;
     gd.gates_sorted = ws.gates_sorted;
-    {
+    if (decode_slot_grouping(T, K, E, H, I)) {
+      // One workgroup ranks and groups the routes and publishes the slot
+      // table; every gate/up workgroup then reads its slot.
+      {
+        StageScope st(TFM_STAGE_TOPK, s);
+        launch_ds_route_group(f16, g.route, ws.logits, T, E, K, ws.idx, ws.gates, gd, &ws.hdr->status, s);
+      }
+      StageScope st(TFM_STAGE_GATEUP, s);
+      const RowMap rmx{gd.order, nullptr, K, T, &ws.hdr->status};
+      launch_gemv_gateup(f16, static_cast<const uint16_t*>(x), rmx, gd, (int)(R < E ? R : E), R,
+                         weights->gate, weights->up, I, H, ws.h, s);
+    } else {
+      // Top-k over many workgroups; every gate/up workgroup groups the routes
+      // itself, and its first publishes the grouping for the down GEMV.
+      {
+        StageScope st(TFM_STAGE_TOPK, s);
+        launch_topk(g.route, f16, ws.logits, T, E, K, ws.idx, nullptr, ws.gates, s);
+      }
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_decode_gateup(f16, static_cast<const uint16_t*>(x), ws.idx, ws.gates, T, E, K, H, I,
                            weights->gate, weights->up, gd, ws.h, &ws.hdr->status, s);

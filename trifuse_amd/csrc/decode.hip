@@ -9,7 +9,9 @@
 //      expert (stable, in LDS; a few hundred VALU ops) and then streams a few
 //      gate/up row units of one active expert through the dequant GEMV with
 //      the SwiGLU epilogue; workgroup (0, 0) also publishes the grouping for
-//      the next kernels,
+//      the next kernels. (With many gate/up workgroups the block instead runs
+//      one route-and-group workgroup after the logits and the slot-reading
+//      GEMV of gemv.hip: capi.hip, decode_slot_grouping.)
 //   3. the down dequant GEMV scaled by each route's gate (gemv.hip),
 //   4. the ordered K reduction + residual (combine.hip).
 // Each kernel boundary is the only synchronisation: on MI355X a launch costs
@@ -312,12 +314,11 @@ void launch_decode_logits(bool f16, const uint16_t* x, const uint16_t* router, c
   check_hip(hipGetLastError(), "decode logits launch");
 }
 
-void launch_decode_route(int route_kind, bool f16, const uint16_t* x, const uint16_t* router,
-                         const float* bias, int T, int H, int E, int K, uint16_t* logits, int32_t* idx,
-                         float* gates, hipStream_t s) {
-  if (T <= 0) return;
-  launch_decode_logits(f16, x, router, bias, T, H, E, logits, s);
-  launch_topk(route_kind, f16, logits, T, E, K, idx, nullptr, gates, s);
+int decode_gateup_workgroups(int T, int K, int E, int H, int I) {
+  const int lg = lg_for(H);
+  const int ur = 4 * (64 / lg), upe = (I + ur - 1) / ur;
+  const int max_active = T * K < E ? T * K : E;
+  return ((upe + kGemvUnits - 1) / kGemvUnits) * max_active;
 }
 
 void launch_decode_gateup(bool f16, const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,

@@ -1185,10 +1185,13 @@ void launch_ds_down(const uint16_t* hsorted, int H, int I, int max_active, const
 void launch_ds_route_group(int route_kind, const uint16_t* logits, int T, int E, int K, int32_t* idx,
                            float* gates, const Grouping& g, uint32_t* status, hipStream_t s) {
   if (T * K > 256 || E > 64 || T <= 0) fail(TFM_E_INVALID, "route+group: more than 256 routes or 64 experts");
+  // One wave per token up to 16 waves, at least 4 (the grouping's ballots
+  // take 4 waves of 64 routes): fewer waves wait at the grouping's barriers.
+  const int nt = 64 * (T < 4 ? 4 : T > 16 ? 16 : T);
   if (route_kind == TFM_ROUTE_OLMOE)
-    tfm_launch(ds_route_group_kernel<TFM_ROUTE_OLMOE>, 1, 1024, 0, s, logits, T, E, K, idx, gates, g, status);
+    tfm_launch(ds_route_group_kernel<TFM_ROUTE_OLMOE>, 1, nt, 0, s, logits, T, E, K, idx, gates, g, status);
   else
-    tfm_launch(ds_route_group_kernel<TFM_ROUTE_GRANITE>, 1, 1024, 0, s, logits, T, E, K, idx, gates, g, status);
+    tfm_launch(ds_route_group_kernel<TFM_ROUTE_GRANITE>, 1, nt, 0, s, logits, T, E, K, idx, gates, g, status);
   check_hip(hipGetLastError(), "route+group launch");
 }
 

@@ -136,9 +136,6 @@ void launch_rmsnorm(bool f16, const uint16_t* x, const uint16_t* w, float eps, i
                     uint16_t* out, hipStream_t s);
 
 // Decode path (decode.hip), T*K <= 256 routes.
-void launch_decode_route(int route_kind, bool f16, const uint16_t* x, const uint16_t* router, const float* bias,
-                         int T, int H, int E, int K, uint16_t* logits, int32_t* idx, float* gates,
-                         hipStream_t s);
 // The decode logits on the affine router itself (bits 4 or 8), each row
 // dequantised in the kernel as the dequant pass would round it; false (nothing
 // launched) for a hidden size without a variant.
@@ -237,6 +234,9 @@ inline void launch_ds_route_group(bool f16, int route_kind, const uint16_t* logi
 #undef TFM_DS_PICK
 // Also publishes the grouping (g, including g.slots and g.gates_sorted from
 // the flat fp32 `gates`).
+// Workgroups of decode_gateup_kernel's grid (row-unit blocks x active-slot
+// bound) for a batch.
+int decode_gateup_workgroups(int T, int K, int E, int H, int I);
 void launch_decode_gateup(bool f16, const uint16_t* x, const int32_t* idx, const float* gates, int T, int E,
                           int K, int H, int I, const tfm_affine& gate, const tfm_affine& up,
                           const Grouping& g, uint16_t* h, uint32_t* status, hipStream_t s);
