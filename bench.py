@@ -302,6 +302,24 @@ def workload_report(r: Runner, ms_per_step: float, wall_ms: float, stages, graph
     return rep
 
 
+def gemv_gateup_label(g, T: int, bits: int) -> str:
+    """The decode GEMV path's gate/up kernel: with at least 4096 gate/up
+    workgroups (row-unit blocks x active-slot bound) the library publishes a
+    slot table and runs gemv_kernel, else decode_gateup_kernel groups the
+    routes in every workgroup (TFM_DECODE_GROUPING overrides, as in the
+    library)."""
+    o = os.environ.get("TFM_DECODE_GROUPING")
+    if o in ("slots", "workgroup"):
+        slots = o == "slots"
+    else:
+        nch = g.hidden // 32
+        lg = 4 if nch <= 4 else 8 if nch <= 8 else 16 if nch <= 16 else 32 if nch <= 32 else 64
+        ur = 4 * (64 // lg)
+        upe = (g.intermediate + ur - 1) // ur
+        slots = (upe + 1) // 2 * min(T * g.top_k, g.experts) >= 4096
+    return "gemv_kernel<gateup>" if slots else "decode_gateup_kernel"
+
+
 def dominant_roofline(r: Runner, stages):
     """Roofline object for the gate/up kernel (the largest share of bytes and FLOPs)."""
     from trifuse_amd import workload as wl
@@ -344,7 +362,7 @@ def dominant_roofline(r: Runner, stages):
         pf_on = os.environ.get("TFM_DS_PREFETCH") == "1"
         prefetch = (sum(U) / len(U) * dn_bytes_expert) if (pf_on and streaming and T <= 3 and R <= 24) else 0.0
         achieved = (per_launch + prefetch) / dur_s / 1e9
-        label = "ds_gateup_kernel" if streaming else "decode_gateup_kernel" if gemv else gemm_label
+        label = "ds_gateup_kernel" if streaming else gemv_gateup_label(g, T, r.wl.bits) if gemv else gemm_label
         return {"kernel": label,
                 "bound": "hbm", "achieved": achieved,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
