@@ -217,12 +217,13 @@ static int ds_max_tokens() {
 // tokens), one route-and-group workgroup publishes the slot table after the
 // logits and every gate/up workgroup reads its slot (gemv_kernel); with few
 // (Granite), the multi-workgroup top-k runs instead and every gate/up
-// workgroup groups the routes itself (decode_gateup_kernel): the single
-// workgroup costs about 1.9 us more than the top-k, and each gate/up
-// workgroup saves about 0.7 us of grouping. Per layer, slots against
-// in-workgroup grouping, one box: OLMoE 4 tokens 39.3 against 39.4 us,
-// 8 tokens (16 layers) 53.6 against 55.5, 12 tokens 64.1 against 65.4;
-// Granite 4 tokens 27.8 against 26.3, 8 tokens 34.2 against 33.2.
+// workgroup groups the routes itself (decode_gateup_kernel). Reading a slot
+// instead of grouping shortens each gate/up workgroup's prologue (1.7 us of
+// route-id read and grouping at batch 8), which pays off only over many
+// workgroups. Per layer, slots against in-workgroup grouping, one box:
+// OLMoE 4 tokens 39.3 against 39.4 us, 8 tokens (16 layers) 53.6 against
+// 55.5, 12 tokens 64.1 against 65.4; Granite 4 tokens 27.8 against 26.3,
+// 8 tokens 34.2 against 33.2.
 static bool decode_slot_grouping(int T, int K, int E, int H, int I) {
   static const int o = [] {
     const char* s = std::getenv("TFM_DECODE_GROUPING");
@@ -426,7 +427,8 @@ static void run_experts(const tfm_plan* p, const uint16_t* x, int64_t T, const u
     {
       StageScope st(TFM_STAGE_GATEUP, s);
       launch_ds_gateup(f16, g.bits, kDsGivenRoutes, x, nullptr, const_cast<int32_t*>(idx), const_cast<float*>(gates),
-                       (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s, &w->down);
+                       (int)T, K, E, H, I, w->gate, w->up, gd, &ws.hdr->status, ws.h, s,
+                       ds_prefetch() ? &w->down : nullptr);
     }
     if (decode_small((int)T, K)) {
       StageScope st(TFM_STAGE_DOWN, s);
