@@ -539,12 +539,24 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
   // x row is staged before any weight load is issued, so that waiting for it
   // does not wait for those loads.
   const bool one = MODE != kDsGiven && T == 1;
+  // Two to four tokens with ranked routes (at most 64 routes): wave t < T
+  // ranks token t and hands its chosen-id mask to the others through LDS;
+  // after one barrier every wave reads the grouping off the T masks. Route
+  // (t, k) to expert e sits at sorted position off(e) + (tokens before t that
+  // chose e), off(e) = the routes of all tokens to experts below e. No
+  // grouping scratch, so the x rows are staged before that barrier.
+  const bool few = MODE != kDsGiven && T >= 2 && T <= 4 && T <= NT / 64 && R <= 64;
+  const int wave = uni(tid >> 6);
+  __shared__ uint64_t s_fmask[4];
+  __shared__ int s_fid[64];
+  uint64_t fm0 = 0, fm1 = 0, fm2 = 0, fm3 = 0;  // few tokens: chosen-id masks of tokens 0-3
+  int off_e = 0;                                 // few tokens: routes to experts below lane e
   const bool hro = ds_h_route_order(MODE, T, K);  // h rows in route order
   int pf_e = -1;  // route f's expert in lane f, for the down-weight prefetch
   int4 sl = make_int4(-1, 0, 0, 0);
   uint64_t chosen = 0;          // one token: mask of the chosen ids
-  float gv = 0.0f;              // one token: lane f's gate
-  int id = -1, pos = 0, ex = -1;  // one token: lane f's id and sorted position; lane a's expert
+  float gv = 0.0f;              // one or few tokens: lane f's (lane k's) gate
+  int id = -1, pos = 0, ex = -1;  // one or few tokens: the route's id and sorted position; lane a's expert
   int ordv = 0;                   // one token: lane a's route
   if (one) {
     if (MODE == TFM_ROUTE_OLMOE) {
@@ -561,6 +573,49 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     sl = lane < K ? make_int4(ex, lane, lane + 1, K) : make_int4(-1, 0, 0, K);
     if (A.pf.q != nullptr && route) pf_e = id;
     stage_x();
+  } else if (few) {
+    if (wave < T) {
+      uint64_t ch = 0;
+      if (MODE == TFM_ROUTE_OLMOE) {
+        uint16_t gb;
+        id = olmoe_route_wave<kF16>(A.logits + (int64_t)wave * E, E, K, &gv, &gb, &ch);
+      } else {
+        id = granite_route_wave<kF16>(A.logits + (int64_t)wave * E, E, K, &gv, &ch);
+      }
+      if (lane == 0) s_fmask[wave] = ch;
+      if (lane < K) s_fid[wave * K + lane] = id;
+    }
+    stage_x();
+    __syncthreads();  // masks, route ids and x rows visible
+    auto uni64 = [](uint64_t v) {
+      return (uint64_t)(uint32_t)uni((int)(uint32_t)v) | ((uint64_t)(uint32_t)uni((int)(v >> 32)) << 32);
+    };
+    fm0 = uni64(s_fmask[0]);
+    fm1 = uni64(s_fmask[1]);
+    fm2 = T > 2 ? uni64(s_fmask[2]) : 0ull;
+    fm3 = T > 3 ? uni64(s_fmask[3]) : 0ull;
+    const uint64_t um = fm0 | fm1 | fm2 | fm3;
+    const int U = __popcll(um);
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    off_e = __popcll(fm0 & below) + __popcll(fm1 & below) + __popcll(fm2 & below) + __popcll(fm3 & below);
+    const int cnt_e = (int)((fm0 >> lane) & 1) + (int)((fm1 >> lane) & 1) + (int)((fm2 >> lane) & 1) +
+                      (int)((fm3 >> lane) & 1);
+    // Lane e of the union goes to slot a = union ids below e; the other lanes
+    // to the slots past U, so that the permute's targets are distinct.
+    const bool in = (um >> lane) & 1;
+    const int a = __popcll(um & below);
+    const int dst = 4 * (in ? a : U + (lane - a));
+    ex = __builtin_amdgcn_ds_permute(dst, in ? lane : -1);
+    const int j0a = __builtin_amdgcn_ds_permute(dst, off_e);
+    const int j1a = __builtin_amdgcn_ds_permute(dst, off_e + cnt_e);
+    sl = lane < U ? make_int4(ex, j0a, j1a, U) : make_int4(-1, 0, 0, U);
+    if (A.pf.q != nullptr && lane < R) pf_e = s_fid[lane];
+    if (wave < T && lane < K) {
+      const uint64_t bl = (1ull << id) - 1ull;
+      pos = __popcll(fm0 & bl) + __popcll(fm1 & bl) + __popcll(fm2 & bl) + __popcll(fm3 & bl) +
+            (wave > 0 ? (int)((fm0 >> id) & 1) : 0) + (wave > 1 ? (int)((fm1 >> id) & 1) : 0) +
+            (wave > 2 ? (int)((fm2 >> id) & 1) : 0);
+    }
   } else {
     ds_rank_group<MODE>(GL, A.logits, T, E, K, A.idx, A.gates, blockIdx.x == 0, A.grp, A.status);
     __syncthreads();
@@ -646,6 +701,33 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
         A.grp.active[E] = K;
       }
     }
+  } else if (few) {
+    if (wr.i0 < wr.i1) load(wA, wr.i0);
+    if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
+    // The grouping, published as ds_rank_group publishes it.
+    if (blockIdx.x == 0) {
+      if (wave < T && lane < K) {
+        const int f = wave * K + lane;
+        A.idx[f] = id;
+        A.gates[f] = gv;
+        A.grp.order[pos] = f;
+        A.grp.inverse[f] = pos;
+        A.grp.gates_sorted[pos] = gv;
+      }
+      if (wave == 0) {
+        const int U = sl.w;
+        if (lane < E) {
+          A.grp.offsets[lane] = off_e;
+          A.grp.slots[lane] = sl;
+        }
+        if (lane < U) A.grp.active[lane] = ex;
+        if (lane == 0) {
+          A.grp.offsets[E] = R;
+          A.grp.active[E] = U;
+        }
+      }
+    }
+    if (!CW) prefetch();
   } else {
     if (wr.i0 < wr.i1) load(wA, wr.i0);
     if (PIPE == 2 && wr.i0 + 1 < wr.i1) load(wB, wr.i0 + 1);
@@ -677,9 +759,20 @@ __global__ __launch_bounds__(NT + 64 * CW) void ds_gateup_kernel(DsGateUpArgs A)
     // slot); else the sorted position, which the separate down kernel reads.
     // Read once per item: a read per route raised the kernel to 191 registers.
     const int hr0 = hro ? uni(readlane_i(ordv, a)) : j0;
+    // Few tokens: slot a's expert, whose routes are in token order.
+    const int ea = few ? uni(readlane_i(wr.sl.x, a)) : 0;
     for (int j = j0; j < j1; ++j) {
       float ag, au;
-      ds_gu_dot<C>(w, xs, xsum, one ? 0 : s_tok[j], ll, ag, au);
+      int tok = 0;
+      if (few) {
+        // the (j - j0)-th token that chose expert ea
+        int r = j - j0;
+        const bool c0 = (fm0 >> ea) & 1, c1 = (fm1 >> ea) & 1, c2 = (fm2 >> ea) & 1;
+        tok = c0 && r == 0 ? 0 : (r -= c0, c1 && r == 0 ? 1 : (r -= c1, c2 && r == 0 ? 2 : 3));
+      } else if (!one) {
+        tok = s_tok[j];
+      }
+      ds_gu_dot<C>(w, xs, xsum, tok, ll, ag, au);
       emit(hr0 + (j - j0), n, ag, au);
     }
     if (i + PIPE < wr.i1) load(w, i + PIPE);
