@@ -63,7 +63,7 @@ def _check(geom, T, bits=4, dtype=F16, rm=1.0, tag="f16", layer_id=0, router_bit
 # decode GEMV kernels; beyond: grouped GEMM.
 @pytest.mark.parametrize("geom_name,T", [("olmoe", 1), ("olmoe", 4), ("olmoe", 8), ("olmoe", 22),
                                          ("olmoe", 23), ("olmoe", 512), ("granite", 1), ("granite", 5),
-                                         ("granite", 300)])
+                                         ("granite", 32), ("granite", 300)])
 def test_block_f16_affine_router(gpu, geom_name, T):
     geom = wl.OLMOE if geom_name == "olmoe" else wl.GRANITE
     log(f"moe f16 affine router {geom_name} T={T}")
