@@ -15,9 +15,13 @@ from trifuse_amd import workload as wl
 # Granite tokens take the grouped GEMM at 32, 16 and 8 quantisation groups
 # per row (the scale/bias layouts of TFM_GGEMM_SB_LAYOUT); 8 tokens take the
 # decode GEMV kernels (OLMoE with the published slot table, Granite with the
-# grouping in every gate/up workgroup: TFM_DECODE_GROUPING swaps them).
+# grouping in every gate/up workgroup: TFM_DECODE_GROUPING swaps them); 32
+# tokens of either take 64-row tiles of at most 16 rows, which keep their
+# weights two super-steps ahead (TFM_GGEMM_FEW_ROWS=0 one, as the other
+# tiles do; =2 also runs the 300 OLMoE and 64 Granite tokens through that
+# instance).
 CASES = [("olmoe", 1), ("olmoe", 2), ("granite", 1), ("olmoe", 300), ("granite", 64), ("olmoe", 8),
-         ("granite", 8)]
+         ("granite", 8), ("olmoe", 32), ("granite", 32)]
 
 
 def outputs(device="cuda:0"):

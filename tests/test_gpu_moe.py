@@ -83,25 +83,30 @@ def test_olmoe_decode_t8_x16(gpu):
         del layer
 
 
-@pytest.mark.parametrize("T", [3, 4, 13, 14, 15, 22, 23, 24, 32, 33, 64])
+@pytest.mark.parametrize("T", [3, 4, 13, 14, 15, 22, 23, 24, 32, 33, 64, 96, 97])
 def test_olmoe_batch_sweep(gpu, T):
     """Both sides of the streaming-decode (up to 3 tokens), decode-GEMV (up to
     E + 40 = 104 routes, 13 tokens) and grouped-GEMM path switches, the last
     size whose staged x rows would fit the streaming kernels (14 tokens) and
-    the GEMM's 64-row tiles, every token checked."""
+    the GEMM's 64-row tiles, up to and past 12 routes per expert (96 and 97
+    tokens), the limit of the 64-row instance whose tiles of at most 16 rows
+    keep their weights two super-steps ahead; every token checked."""
     w = wl.get_workload(f"olmoe_t{T}")
     log(f"moe {w.name}")
     layer = wl.workload_layers(w, gpu)[0]
     _check_layer(w.geometry, _block(w.geometry), wl.workload_x(w), layer, None)
 
 
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 10, 11, 19, 20, 22, 23])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 10, 11, 19, 20, 22, 23, 60, 61])
 def test_granite_batch_sweep(gpu, T):
     """Granite (hidden 1536, 40 experts), every token checked: the one- and
     two-token streaming layers, the four-kernel streaming layer (3 tokens),
     the decode GEMV from 4 tokens up to E + 40 = 80 routes (10 tokens) and the
     grouped GEMM's four-wave 64-row tiles beyond (11 tokens; 19 and 20 tokens
-    on either side of the streaming kernels' LDS limit; 23 tokens)."""
+    on either side of the streaming kernels' LDS limit; 23 tokens; 60 and 61
+    tokens on either side of 12 routes per expert, the limit of the instance
+    whose tiles of at most 16 rows keep their weights two super-steps
+    ahead)."""
     w = wl.get_workload(f"granite_t{T}")
     log(f"moe {w.name}")
     layer = wl.workload_layers(w, gpu)[0]

@@ -569,7 +569,7 @@ __device__ __forceinline__ f32x4_t mfma16(f16x8_t a, f16x8_t b, f32x4_t c, std::
 // leave compute units idle (a few experts or a few output columns: Granite
 // decode batches, a dense matrix); 48 KB of LDS, three workgroups per
 // compute unit.
-template <int BM, int MODE, bool F16, int WV>
+template <int BM, int MODE, bool F16, int WV, bool FEW = false>
 __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void ggemm_wr_kernel(GgArgs args) {
   constexpr int WAVES = WV, BN = 32 * WV;
   constexpr int MB = BM / 16;                     // 16-row blocks per wave
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
   const uint32_t a_lane = (uint32_t)((lane & 15) * BK2 * 2 + (((4 * g4) ^ (lane & 15)) << 4));
   auto compute = [&](auto mbl_tag, const uint16_t* A, op_t* b, const uint4* rc, const float* sc,
                      const float* bic, const uint4* rn, const float* sn, const float* bin, uint16_t* An,
-                     int ktn) __attribute__((always_inline)) {
+                     int ktn, auto after_copy) __attribute__((always_inline)) {
     constexpr int MBL = decltype(mbl_tag)::value;
     constexpr int NQ = 4 * MBL, D = 3, R = D + 1;
     constexpr int CR = 4 * WAVES;  // rows per copy round
@@ -830,6 +830,7 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
     static_for<0, NQ>([&](auto q_) {
       constexpr int q = decltype(q_)::value, s = q / MBL, i = q % MBL;
       if constexpr (q % STEP == 0 && q / STEP < NC) a_copy1(An, ktn, std::integral_constant<int, q / STEP>{});
+      if constexpr (q == STEP * (NC - 1)) after_copy();
       if constexpr (q + D < NQ) rd(std::integral_constant<int, q + D>{});
       acc[i][0] = mfma16(af[q % R], b[0], acc[i][0], f16tag{});
       acc[i][1] = mfma16(af[q % R], b[1], acc[i][1], f16tag{});
@@ -861,6 +862,46 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
     });
   };
 
+  // ---- few rows (FEW instances): weights two super-steps ahead ----
+  // In the loop below every super-step ends at a barrier that waits for all
+  // of its loads, and the raw weights of super-step k+1 (whose first word
+  // the last sub-step of super-step k dequantises) are requested at the start
+  // of super-step k: one super-step of loads in flight. A tile of at most 16
+  // rows (one row block) has too few MFMAs per super-step to cover a memory
+  // latency that way. Here the raw weights of super-step k+2 are requested
+  // right after the activation copy of super-step k+1, and the barrier waits
+  // only for that copy (the vector memory counter retires in issue order), so
+  // they stay in flight across it. The products and their order are those of
+  // the loop below.
+  if (FEW && rows_valid <= 16 && (KT & 3) == 0) {
+    if constexpr (FEW) {
+      static_assert(BM == 64, "few-row tiles are 64-row tiles");
+      uint4 rw[4][2];                             // raw weights of super-step k in slot k % 4
+      float fsc[2][2], fbi[2][2];                 // scales and biases of super-step k in set k % 2
+      op_t fb[2];
+      a_copy(sA0, 0);
+      bload(rw[0], 0);
+      bload(rw[1], 1);
+      __syncthreads();  // scale copies and stage 0 complete and visible
+      sb_read(fsc[0], fbi[0], 0);
+      deq(fb, rw[0], fsc[0], fbi[0], 0);
+      for (int kt0 = 0; kt0 < KT; kt0 += 4) {
+        static_for<0, 4>([&](auto q_) {
+          constexpr int q = decltype(q_)::value, c = q % 2, n = 1 - c;
+          const int kt = kt0 + q;
+          uint16_t* const A = c == 0 ? sA0 : sA1;
+          uint16_t* const An = c == 0 ? sA1 : sA0;
+          sb_read(fsc[n], fbi[n], kt + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(std::integral_constant<int, 1>{}, A, fb, rw[q], fsc[c], fbi[c], rw[(q + 1) % 4], fsc[n],
+                  fbi[n], An, kt + 1, [&] { bload(rw[(q + 2) % 4], kt + 2); });
+          // This wave's copy into An is done (only the two weight loads
+          // issued after it may be outstanding), then every wave's.
+          asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
+        });
+      }
+    }
+  } else {
   // ---- prologue ----
   uint4 r0[2], r1[2];
   float sc0[2], bi0[2], sc1[2], bi1[2];
@@ -879,12 +920,12 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
       bload(r1, kt + 1);
       sb_read(sc1, bi1, kt + 1);
       __builtin_amdgcn_sched_barrier(0);
-      compute(mbl_tag, sA0, bop, r0, sc0, bi0, r1, sc1, bi1, sA1, kt + 1);
+      compute(mbl_tag, sA0, bop, r0, sc0, bi0, r1, sc1, bi1, sA1, kt + 1, [] {});
       __syncthreads();
       bload(r0, kt + 2);
       sb_read(sc0, bi0, kt + 2);
       __builtin_amdgcn_sched_barrier(0);
-      compute(mbl_tag, sA1, bop, r1, sc1, bi1, r0, sc0, bi0, sA0, kt + 2);
+      compute(mbl_tag, sA1, bop, r1, sc1, bi1, r0, sc0, bi0, sA0, kt + 2, [] {});
       __syncthreads();
     }
   };
@@ -914,6 +955,7 @@ __global__ __launch_bounds__(WV * 64, BM == 64 ? (WV == 8 ? 2 : 3) : 1) void gge
       main_loop(std::integral_constant<int, 2>{});
     else
       main_loop(std::integral_constant<int, 4>{});
+  }
   }
 
   // ---- epilogue ----
@@ -1101,6 +1143,19 @@ static int sb_layout(int Kin) {
   return G == 16 || G == 32 ? kSbChunk : kSbPlain;
 }
 
+// The FEW instance of a 64-row launch (tiles of at most 16 rows keep their
+// weights two super-steps ahead) runs where experts average at most
+// kFewRowsAvg routes, so that most tiles hold at most 16 rows.
+// TFM_GGEMM_FEW_ROWS=0 never uses it, =2 uses it for every 64-row launch.
+constexpr int kFewRowsAvg = 12;
+static bool use_few_rows(int64_t n_routes, int E) {
+  static const int v = [] {
+    const char* s = std::getenv("TFM_GGEMM_FEW_ROWS");
+    return s && (s[0] == '0' || s[0] == '2') && s[1] == 0 ? s[0] - '0' : 1;
+  }();
+  return v == 2 || (v == 1 && n_routes <= (int64_t)E * kFewRowsAvg);
+}
+
 template <int BM, int MODE, bool F16, int WV>
 static void launch_wr_waves(const GgArgs& a_in, int64_t n_routes, int E, hipStream_t s) {
   GgArgs a = a_in;
@@ -1112,6 +1167,12 @@ static void launch_wr_waves(const GgArgs& a_in, int64_t n_routes, int E, hipStre
   // 17); workgroups past their XCD's run exit at once.
   unsigned grid = grid_for(n_routes, E, BM, NT);
   if (BM == 256) grid = ((grid / 8 * 29 + 16) / 17 + 2) * 8;
+  if constexpr (BM == 64) {
+    if (use_few_rows(n_routes, E)) {
+      tfm_launch(ggemm_wr_kernel<BM, MODE, F16, WV, true>, grid, WV * 64, 0, s, a);
+      return;
+    }
+  }
   tfm_launch(ggemm_wr_kernel<BM, MODE, F16, WV>, grid, WV * 64, 0, s, a);
 }
 
