@@ -1167,7 +1167,9 @@ static void launch_wr_waves(const GgArgs& a_in, int64_t n_routes, int E, hipStre
   // 17); workgroups past their XCD's run exit at once.
   unsigned grid = grid_for(n_routes, E, BM, NT);
   if (BM == 256) grid = ((grid / 8 * 29 + 16) / 17 + 2) * 8;
-  if constexpr (BM == 64) {
+  // Not for 8-wave half storage: there the ring would cost a workgroup per
+  // compute unit (three waves per SIMD).
+  if constexpr (BM == 64 && !(F16 && WV == 8)) {
     if (use_few_rows(n_routes, E)) {
       tfm_launch(ggemm_wr_kernel<BM, MODE, F16, WV, true>, grid, WV * 64, 0, s, a);
       return;
