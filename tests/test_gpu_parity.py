@@ -114,8 +114,10 @@ def _routes_reference(x64, tok, eid, lay, dtype):
     return out
 
 
+# N = 8: decode GEMV kernels; 300 (about 5 routes per expert): the grouped
+# GEMM's 64-row tiles, with bf16 the few-row instance; 2400: larger tiles.
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("N", [8, 2400])
+@pytest.mark.parametrize("N", [8, 300, 2400])
 def test_gpu_callable_rows_against_oracle(gpu, dtype, N):
     geom = wl.OLMOE
     tdt = torch.float16 if dtype == "f16" else torch.bfloat16
