@@ -24,9 +24,9 @@
 namespace tfm {
 
 // Standalone decode GEMV over grouped routes (gather_qmm and the MoE block
-// given routes): workgroup (bx, a) (4 waves) streams kGemvUnits row units of
-// active expert a (blockIdx.y indexes the ascending active-expert list).
-template <int LG, int MODE, bool F16>
+// given routes): workgroup (bx, a) (4 waves) streams NU row units of active
+// expert a (blockIdx.y indexes the ascending active-expert list).
+template <int LG, int MODE, bool F16, int NU = kGemvUnits>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x, RowMap rm,
                                                    Grouping g, tfm_affine wa, tfm_affine wb,
                                                    int N, int kin, const float* __restrict__ gates,
@@ -69,8 +69,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
       static_cast<float*>(out)[(int64_t)j * N + n] = a0 * xgate[t];
     }
   };
-  gemv_units<LG, NM, kGemvUnits, F16>(L, x, kin, N, wa, wb, e, j0, j1, blockIdx.x * kGemvUnits, xrow, stage,
+  gemv_units<LG, NM, NU, F16>(L, x, kin, N, wa, wb, e, j0, j1, blockIdx.x * NU, xrow, stage,
                                  emit);
+}
+
+static int64_t gemv_cus() {
+  static const int64_t cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    return n;
+  }();
+  return cus;
 }
 
 template <int MODE, bool F16>
@@ -81,11 +92,24 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   if (Kin % 64 != 0 || Kin <= 0 || Kin > 2048)
     fail(TFM_E_UNSUPPORTED, "affine GEMV: input width must be a multiple of 64 up to 2048");
   const int nch = Kin / 32;
-#define TFM_GEMV_LAUNCH(LGV)                                                                \
+  // Plain products (gather_qmm, the dense linear) with fewer workgroups than
+  // two per compute unit take one row unit per workgroup, twice the
+  // workgroups: the dense 2048 x 2048 linear at one row 4.47 -> 4.06 us, the
+  // 64 x 2048 router 3.2 -> 2.8 us. The MoE block's GEMVs have many
+  // experts' workgroups and keep two units (one measured slower there).
+#define TFM_GEMV_LAUNCH_NU(LGV, NUV)                                                        \
   {                                                                                         \
     const int ur = 4 * (64 / LGV), upe = (N + ur - 1) / ur;                                 \
-    const dim3 grid((unsigned)((upe + kGemvUnits - 1) / kGemvUnits), (unsigned)max_active); \
-    tfm_launch(gemv_kernel<LGV, MODE, F16>, grid, 256, 0, s, x, rm, g, wa, wb, N, Kin, gates, out); \
+    const dim3 grid((unsigned)((upe + NUV - 1) / NUV), (unsigned)max_active);               \
+    tfm_launch(gemv_kernel<LGV, MODE, F16, NUV>, grid, 256, 0, s, x, rm, g, wa, wb, N, Kin, gates, out); \
+  }
+#define TFM_GEMV_LAUNCH(LGV)                                                                    \
+  {                                                                                             \
+    const int64_t ur = 4 * (64 / LGV), upe = (N + ur - 1) / ur;                                 \
+    const bool one = MODE == kPlain &&                                                          \
+                     (int64_t)max_active * ((upe + kGemvUnits - 1) / kGemvUnits) < 2 * gemv_cus(); \
+    if (one) TFM_GEMV_LAUNCH_NU(LGV, 1)                                                         \
+    else TFM_GEMV_LAUNCH_NU(LGV, kGemvUnits)                                                    \
   }
   if (nch <= 4) TFM_GEMV_LAUNCH(4)
   else if (nch <= 8) TFM_GEMV_LAUNCH(8)
@@ -93,6 +117,7 @@ static void dispatch_gemv(int Kin, const uint16_t* x, RowMap rm, const Grouping&
   else if (nch <= 32) TFM_GEMV_LAUNCH(32)
   else TFM_GEMV_LAUNCH(64)
 #undef TFM_GEMV_LAUNCH
+#undef TFM_GEMV_LAUNCH_NU
   check_hip(hipGetLastError(), "gemv launch");
 }
 
